@@ -1,0 +1,450 @@
+// C ABI of the gfx950 FP8 MoE path (declarations: include/hkmoe.h).
+//
+// Host code: argument validation (before any launch), launch configuration,
+// workspace carving and stream-ordered enqueueing.  No host synchronisation and
+// no allocation happens in any entry point: callers own every buffer, as with
+// the reference's dispatch functions (include/pyutils/pyutils.cuh:54-71,
+// kernels/cdna3/.../256_256_64_32.cpp:202-206).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/hkmoe.h"
+#include "gemm_fp8.hpp"
+#include "moe_kernels.hpp"
+
+using namespace hkmoe;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(HKMOE_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+  return HKMOE_OK;
+}
+
+#define HK_REQUIRE(cond, ...)                                 \
+  do {                                                        \
+    if (!(cond)) return fail(HKMOE_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+#define HK_TRY(expr)               \
+  do {                             \
+    const int _rc = (expr);        \
+    if (_rc != HKMOE_OK) return _rc; \
+  } while (0)
+
+constexpr int kMaxDevices = 64;
+
+int device_cus() {
+  static int cus[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+template <Epi EPI, Scale SC>
+int launch_gemm(const GemmParams& p, hipStream_t stream) {
+  static bool attr_set[kMaxDevices] = {false};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  auto kern = gemm_fp8_persistent<EPI, SC>;
+  if (dev >= 0 && dev < kMaxDevices && !attr_set[dev]) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (err != hipSuccess) return fail(HKMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(err));
+    attr_set[dev] = true;
+  }
+  const int grid = device_cus();
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), kLdsBytes, stream, p);
+  return check_launch("gemm_fp8_persistent");
+}
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+int route_blocks(int64_t t) { return static_cast<int>((t + kRouteTok - 1) / kRouteTok); }
+
+int pow2_at_least(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hkmoe_version(void) { return 100; }
+
+const char* hkmoe_last_error(void) { return g_last_error.c_str(); }
+
+int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+                   const float* scale_a, const float* scale_b, int out_dtype, hkmoe_stream_t stream) {
+  HK_REQUIRE(a && b && c, "gemm_fp8: null tensor pointer");
+  HK_REQUIRE(m >= 0 && n > 0 && k > 0, "gemm_fp8: bad shape M=%lld N=%lld K=%lld", (long long)m,
+             (long long)n, (long long)k);
+  HK_REQUIRE(k % kBK == 0, "gemm_fp8: K=%lld must be a multiple of 128", (long long)k);
+  HK_REQUIRE(n % kBN == 0, "gemm_fp8: N=%lld must be a multiple of 256", (long long)n);
+  HK_REQUIRE(k <= (1 << 20) && n * k < (1ll << 32) && m < (1ll << 31),
+             "gemm_fp8: operand too large for 32-bit buffer offsets");
+  HK_REQUIRE(out_dtype == HKMOE_BF16 || out_dtype == HKMOE_F32, "gemm_fp8: bad out_dtype %d", out_dtype);
+  if (m == 0) return HKMOE_OK;
+  GemmParams p{};
+  p.a = static_cast<const uint8_t*>(a);
+  p.b = static_cast<const uint8_t*>(b);
+  p.c = c;
+  p.a_scale = scale_a;
+  p.b_scale = scale_b;
+  p.rows = m;
+  p.num_experts = 1;
+  p.K = static_cast<int32_t>(k);
+  p.nb = static_cast<int32_t>(n);
+  p.n_out = static_cast<int32_t>(n);
+  p.n_tiles = static_cast<int32_t>(n / kBN);
+  auto s = static_cast<hipStream_t>(stream);
+  return out_dtype == HKMOE_BF16 ? launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s)
+                                 : launch_gemm<Epi::kStoreF32, Scale::kTensor>(p, s);
+}
+
+int hkmoe_route_blocks(int64_t num_tokens) { return route_blocks(num_tokens); }
+
+int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                     int32_t* topk_idx, float* topk_w, int32_t* block_counts, hkmoe_stream_t stream) {
+  HK_REQUIRE(logits && topk_idx && topk_w && block_counts, "route_topk: null pointer");
+  HK_REQUIRE(num_tokens >= 0 && num_tokens < (1ll << 31) / kMaxTopK, "route_topk: bad T=%lld",
+             (long long)num_tokens);
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "route_topk: E=%d outside [1, %d]",
+             num_experts, kMaxExperts);
+  HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK,
+             "route_topk: top_k=%d outside [1, min(E, %d)]", top_k, kMaxTopK);
+  if (num_tokens == 0) return HKMOE_OK;
+  hipLaunchKernelGGL(route_topk_kernel, dim3(route_blocks(num_tokens)), dim3(kRouteThreads), 0,
+                     static_cast<hipStream_t>(stream), logits, static_cast<int>(num_tokens),
+                     num_experts, top_k, topk_idx, topk_w, block_counts);
+  return check_launch("route_topk_kernel");
+}
+
+int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
+                         int32_t* counts, int32_t* offsets, int32_t* block_base,
+                         int32_t* mtile_offsets, float* amax_reset, hkmoe_stream_t stream) {
+  HK_REQUIRE(counts && offsets && block_base && mtile_offsets, "expert_offsets: null pointer");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "expert_offsets: E=%d outside [1, %d]",
+             num_experts, kMaxExperts);
+  HK_REQUIRE(num_tokens >= 0, "expert_offsets: bad T");
+  HK_REQUIRE(num_tokens == 0 || block_counts, "expert_offsets: null block_counts");
+  const int nblk = route_blocks(num_tokens);
+  const int e_stride = pow2_at_least(num_experts);
+  const int parts = kScanThreads / e_stride;
+  hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(kScanThreads), 0,
+                     static_cast<hipStream_t>(stream), block_counts, nblk, num_experts, e_stride,
+                     parts, counts, offsets, block_base, mtile_offsets, kBM, amax_reset);
+  return check_launch("expert_offsets_kernel");
+}
+
+int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                  const int32_t* offsets, const int32_t* block_base, int32_t* perm, int32_t* inv_perm,
+                  const void* x_q, const float* x_scale, int64_t hidden, int scale_mode, void* xp,
+                  float* xp_scale_t, hkmoe_stream_t stream) {
+  HK_REQUIRE(topk_idx && offsets && block_base && perm && inv_perm, "scatter: null pointer");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "scatter: E=%d outside [1, %d]",
+             num_experts, kMaxExperts);
+  HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK, "scatter: bad top_k=%d", top_k);
+  HK_REQUIRE(num_tokens >= 0, "scatter: bad T");
+  HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
+             "scatter: bad scale_mode %d", scale_mode);
+  if (x_q != nullptr) {
+    HK_REQUIRE(xp != nullptr, "scatter: x_q given without xp");
+    HK_REQUIRE(hidden > 0 && hidden % 16 == 0, "scatter: hidden=%lld must be a multiple of 16",
+               (long long)hidden);
+    if (scale_mode == HKMOE_SCALE_BLOCK) {
+      HK_REQUIRE(hidden % kGroup == 0, "scatter: hidden must be a multiple of 128 for block scales");
+      HK_REQUIRE(x_scale && xp_scale_t, "scatter: block scales need x_scale and xp_scale_t");
+    }
+  }
+  if (num_tokens == 0) return HKMOE_OK;
+  hipLaunchKernelGGL(scatter_kernel, dim3(route_blocks(num_tokens)), dim3(kRouteThreads), 0,
+                     static_cast<hipStream_t>(stream), topk_idx, static_cast<int>(num_tokens),
+                     num_experts, top_k, offsets, block_base, perm, inv_perm,
+                     static_cast<const uint8_t*>(x_q), x_scale, hidden,
+                     scale_mode == HKMOE_SCALE_BLOCK ? 1 : 0, static_cast<uint8_t*>(xp), xp_scale_t,
+                     num_tokens * top_k);
+  return check_launch("scatter_kernel");
+}
+
+int hkmoe_grouped_gemm1(const void* xp, const float* xp_scale, const void* w13,
+                        const float* w13_scale, const int32_t* offsets, const int32_t* mtile_offsets,
+                        int64_t rows, int32_t num_experts, int32_t hidden, int32_t inter,
+                        int scale_mode, void* h, float* amax, hkmoe_stream_t stream) {
+  HK_REQUIRE(xp && w13 && offsets && mtile_offsets && h, "grouped_gemm1: null pointer");
+  HK_REQUIRE(xp_scale && w13_scale, "grouped_gemm1: null scale pointer");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1: bad E=%d", num_experts);
+  HK_REQUIRE(hidden > 0 && hidden % kBK == 0, "grouped_gemm1: hidden=%d must be a multiple of 128", hidden);
+  HK_REQUIRE(inter > 0 && inter % 128 == 0, "grouped_gemm1: inter=%d must be a multiple of 128", inter);
+  HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm1: bad rows");
+  HK_REQUIRE(2ll * inter * hidden < (1ll << 32), "grouped_gemm1: expert weight too large");
+  HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
+             "grouped_gemm1: bad scale_mode %d", scale_mode);
+  if (rows == 0) return HKMOE_OK;
+  GemmParams p{};
+  p.a = static_cast<const uint8_t*>(xp);
+  p.b = static_cast<const uint8_t*>(w13);
+  p.c = h;
+  p.a_scale = xp_scale;
+  p.b_scale = w13_scale;
+  p.offsets = offsets;
+  p.mtile_offsets = mtile_offsets;
+  p.amax = amax;
+  p.rows = rows;
+  p.a_scale_ld = rows;
+  p.num_experts = num_experts;
+  p.K = hidden;
+  p.nb = 2 * inter;
+  p.n_out = inter;
+  p.n_tiles = inter / 128;
+  auto s = static_cast<hipStream_t>(stream);
+  return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kSiluBf16, Scale::kBlock>(p, s)
+                                         : launch_gemm<Epi::kSiluBf16, Scale::kTensor>(p, s);
+}
+
+int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, const float* amax,
+                  void* hq, float* hs, hkmoe_stream_t stream) {
+  HK_REQUIRE(h && hq && hs, "requant: null pointer");
+  HK_REQUIRE(inter > 0 && inter % 128 == 0, "requant: inter=%d must be a multiple of 128", inter);
+  HK_REQUIRE(rows >= 0, "requant: bad rows");
+  auto s = static_cast<hipStream_t>(stream);
+  if (scale_mode == HKMOE_SCALE_BLOCK) {
+    if (rows == 0) return HKMOE_OK;
+    HK_REQUIRE(rows < (1ll << 31), "requant: too many rows");
+    hipLaunchKernelGGL(requant_group_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(h), rows, inter, static_cast<uint8_t*>(hq), hs);
+    return check_launch("requant_group_kernel");
+  }
+  HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR, "requant: bad scale_mode %d", scale_mode);
+  HK_REQUIRE(amax != nullptr, "requant: per-tensor mode needs amax");
+  const int64_t n8 = rows * inter / 8;
+  const int grid = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, (n8 + 255) / 256), 4 * 1024));
+  hipLaunchKernelGGL(requant_tensor_kernel, dim3(grid), dim3(256), 0, s,
+                     static_cast<const uint16_t*>(h), n8, amax, static_cast<uint8_t*>(hq), hs);
+  return check_launch("requant_tensor_kernel");
+}
+
+int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
+                        const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
+                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode, void* y,
+                        hkmoe_stream_t stream) {
+  HK_REQUIRE(hq && hs && w2 && w2_scale && offsets && mtile_offsets && y, "grouped_gemm2: null pointer");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2: bad E=%d", num_experts);
+  HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2: hidden=%d must be a multiple of 256", hidden);
+  HK_REQUIRE(inter > 0 && inter % kBK == 0, "grouped_gemm2: inter=%d must be a multiple of 128", inter);
+  HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm2: bad rows");
+  HK_REQUIRE(static_cast<int64_t>(hidden) * inter < (1ll << 32), "grouped_gemm2: expert weight too large");
+  HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
+             "grouped_gemm2: bad scale_mode %d", scale_mode);
+  if (rows == 0) return HKMOE_OK;
+  GemmParams p{};
+  p.a = static_cast<const uint8_t*>(hq);
+  p.b = static_cast<const uint8_t*>(w2);
+  p.c = y;
+  p.a_scale = hs;
+  p.b_scale = w2_scale;
+  p.offsets = offsets;
+  p.mtile_offsets = mtile_offsets;
+  p.rows = rows;
+  p.a_scale_ld = rows;
+  p.num_experts = num_experts;
+  p.K = inter;
+  p.nb = hidden;
+  p.n_out = hidden;
+  p.n_tiles = hidden / kBN;
+  auto s = static_cast<hipStream_t>(stream);
+  return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kStoreBf16, Scale::kBlock>(p, s)
+                                         : launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s);
+}
+
+int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, int64_t num_tokens,
+                  int32_t top_k, int32_t hidden, void* out, hkmoe_stream_t stream) {
+  HK_REQUIRE(y && topk_w && inv_perm && out, "combine: null pointer");
+  HK_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, "combine: bad top_k=%d", top_k);
+  HK_REQUIRE(hidden > 0 && hidden % 8 == 0, "combine: hidden=%d must be a multiple of 8", hidden);
+  HK_REQUIRE(num_tokens >= 0 && num_tokens < (1ll << 31), "combine: bad T");
+  if (num_tokens == 0) return HKMOE_OK;
+  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(num_tokens)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(y), topk_w,
+                     inv_perm, top_k, hidden, static_cast<uint16_t*>(out));
+  return check_launch("combine_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// whole layer
+// ---------------------------------------------------------------------------
+namespace {
+struct MoeWorkspace {
+  int32_t* topk_idx;
+  float* topk_w;
+  int32_t* block_counts;
+  int32_t* block_base;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* mtile_offsets;
+  float* amax;
+  int32_t* perm;
+  int32_t* inv_perm;
+  uint8_t* xp;
+  float* xps_t;
+  uint16_t* h;
+  uint8_t* hq;
+  float* hs;
+  uint16_t* y;
+  size_t bytes;
+};
+
+MoeWorkspace carve(uint8_t* base, int64_t t, int32_t e, int32_t k, int32_t hidden, int32_t inter,
+                   bool block) {
+  MoeWorkspace w{};
+  size_t off = 0;
+  const int64_t r = t * k;
+  const int64_t nblk = route_blocks(t);
+  auto take = [&](size_t bytes) -> uint8_t* {
+    uint8_t* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  w.topk_idx = reinterpret_cast<int32_t*>(take(r * 4));
+  w.topk_w = reinterpret_cast<float*>(take(r * 4));
+  w.block_counts = reinterpret_cast<int32_t*>(take(nblk * e * 4));
+  w.block_base = reinterpret_cast<int32_t*>(take(nblk * e * 4));
+  w.counts = reinterpret_cast<int32_t*>(take(e * 4));
+  w.offsets = reinterpret_cast<int32_t*>(take((e + 1) * 4));
+  w.mtile_offsets = reinterpret_cast<int32_t*>(take((e + 1) * 4));
+  w.amax = reinterpret_cast<float*>(take(4));
+  w.perm = reinterpret_cast<int32_t*>(take(r * 4));
+  w.inv_perm = reinterpret_cast<int32_t*>(take(r * 4));
+  w.xp = take(r * hidden);
+  w.xps_t = reinterpret_cast<float*>(take(block ? r * (hidden / kGroup) * 4 : 4));
+  w.h = reinterpret_cast<uint16_t*>(take(r * inter * 2));
+  w.hq = take(r * inter);
+  w.hs = reinterpret_cast<float*>(take(block ? r * (inter / kGroup) * 4 : 4));
+  w.y = reinterpret_cast<uint16_t*>(take(r * hidden * 2));
+  w.bytes = off;
+  return w;
+}
+}  // namespace
+
+size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                                int32_t hidden, int32_t inter, int scale_mode) {
+  if (num_tokens < 0 || num_experts < 1 || top_k < 1 || hidden < 1 || inter < 1) return 0;
+  return carve(nullptr, num_tokens, num_experts, top_k, hidden, inter,
+               scale_mode == HKMOE_SCALE_BLOCK).bytes;
+}
+
+int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
+                      const float* w13_scale, const void* w2, const float* w2_scale,
+                      int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
+                      int32_t inter, int scale_mode, void* out, void* workspace,
+                      size_t workspace_bytes, hkmoe_stream_t stream) {
+  HK_REQUIRE(x_q && x_scale && logits && w13 && w13_scale && w2 && w2_scale && out,
+             "moe_forward: null pointer");
+  HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
+             "moe_forward: bad scale_mode %d", scale_mode);
+  HK_REQUIRE(num_tokens >= 0 && num_tokens * top_k < (1ll << 31), "moe_forward: bad T");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "moe_forward: E=%d outside [1, %d]",
+             num_experts, kMaxExperts);
+  HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK, "moe_forward: bad top_k=%d", top_k);
+  HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "moe_forward: hidden=%d must be a multiple of 256", hidden);
+  HK_REQUIRE(inter > 0 && inter % 128 == 0, "moe_forward: inter=%d must be a multiple of 128", inter);
+  const bool block = scale_mode == HKMOE_SCALE_BLOCK;
+  const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, block);
+  if (workspace == nullptr || workspace_bytes < need.bytes)
+    return fail(HKMOE_ERR_WORKSPACE, "moe_forward: workspace of %zu bytes needed, %zu given", need.bytes,
+                workspace_bytes);
+  HK_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "moe_forward: workspace must be 256-byte aligned");
+  if (num_tokens == 0) return HKMOE_OK;
+  const MoeWorkspace w = carve(static_cast<uint8_t*>(workspace), num_tokens, num_experts, top_k,
+                               hidden, inter, block);
+  const int64_t rows = num_tokens * top_k;
+  HK_TRY(hkmoe_route_topk(logits, num_tokens, num_experts, top_k, w.topk_idx, w.topk_w,
+                          w.block_counts, stream));
+  HK_TRY(hkmoe_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets,
+                              w.block_base, w.mtile_offsets, w.amax, stream));
+  HK_TRY(hkmoe_scatter(w.topk_idx, num_tokens, num_experts, top_k, w.offsets, w.block_base, w.perm,
+                       w.inv_perm, x_q, x_scale, hidden, scale_mode, w.xp, w.xps_t, stream));
+  HK_TRY(hkmoe_grouped_gemm1(w.xp, block ? w.xps_t : x_scale, w13, w13_scale, w.offsets,
+                             w.mtile_offsets, rows, num_experts, hidden, inter, scale_mode, w.h,
+                             w.amax, stream));
+  HK_TRY(hkmoe_requant(w.h, rows, inter, scale_mode, w.amax, w.hq, w.hs, stream));
+  HK_TRY(hkmoe_grouped_gemm2(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, rows, num_experts,
+                             hidden, inter, scale_mode, w.y, stream));
+  HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
+  return HKMOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// quantisers
+// ---------------------------------------------------------------------------
+int hkmoe_quant_group(const float* x, int64_t rows, int64_t cols, void* q, float* s,
+                      hkmoe_stream_t stream) {
+  HK_REQUIRE(x && q && s, "quant_group: null pointer");
+  HK_REQUIRE(rows >= 0 && cols > 0 && cols % kGroup == 0, "quant_group: cols must be a multiple of 128");
+  const int64_t waves = rows * (cols / kGroup);
+  if (waves == 0) return HKMOE_OK;
+  HK_REQUIRE((waves + 3) / 4 < (1ll << 31), "quant_group: too large");
+  hipLaunchKernelGGL(quant_group_kernel, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, rows, cols, static_cast<uint8_t*>(q), s);
+  return check_launch("quant_group_kernel");
+}
+
+int hkmoe_quant_block(const float* x, int64_t batch, int64_t rows, int64_t cols, void* q, float* s,
+                      hkmoe_stream_t stream) {
+  HK_REQUIRE(x && q && s, "quant_block: null pointer");
+  HK_REQUIRE(batch >= 0 && rows > 0 && cols > 0 && rows % kGroup == 0 && cols % kGroup == 0,
+             "quant_block: rows and cols must be multiples of 128");
+  const int64_t blocks = batch * (rows / kGroup) * (cols / kGroup);
+  if (blocks == 0) return HKMOE_OK;
+  HK_REQUIRE(blocks < (1ll << 31), "quant_block: too large");
+  hipLaunchKernelGGL(quant_block_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, rows, cols, static_cast<uint8_t*>(q), s);
+  return check_launch("quant_block_kernel");
+}
+
+int hkmoe_quant_tensor(const float* x, int64_t rows, int64_t cols, void* q, float* s, float* amax_ws,
+                       hkmoe_stream_t stream) {
+  HK_REQUIRE(x && q && s && amax_ws, "quant_tensor: null pointer");
+  HK_REQUIRE(rows >= 0 && cols >= 0, "quant_tensor: bad shape");
+  const int64_t n = rows * cols;
+  auto st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(1), dim3(1), 0, st, amax_ws, 0.0f);
+  HK_TRY(check_launch("fill_f32_kernel"));
+  const int grid = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, (n + 255) / 256), 4096));
+  if (n > 0) {
+    hipLaunchKernelGGL(amax_kernel, dim3(grid), dim3(256), 0, st, x, n, amax_ws);
+    HK_TRY(check_launch("amax_kernel"));
+  }
+  hipLaunchKernelGGL(quant_tensor_kernel, dim3(grid), dim3(256), 0, st, x, n, amax_ws,
+                     static_cast<uint8_t*>(q), s);
+  return check_launch("quant_tensor_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,135 @@
+// Device-side building blocks for the gfx950 FP8 MoE path.
+//
+// Everything here is written for CDNA4 (gfx950) only: 64-lane waves, the
+// v_mfma_f32_16x16x128_f8f6f4 matrix instruction, buffer loads that write
+// straight into LDS (buffer_load_dwordx4 ... lds) and OCP e4m3fn FP8.
+//
+// Reference counterparts (behaviour only, nothing is shared):
+//   fp8 MFMA wrapper      include/cdna4/ops/warp/register/tile/mma.cuh:97-125
+//   buffer resource       include/cdna4/ops/warp/memory/util/util.cuh:72-88
+//   direct global->LDS    include/cdna4/ops/warp/memory/util/util.cuh:117-124
+//   bf16 RNE pack         include/cdna4/common/base_types.cuh:350-358
+//   fp8 convert (SATFINITE RNE) include/cdna4/common/base_types.cuh:423-432
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hkmoe {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define HK_LDS __attribute__((address_space(3)))
+
+constexpr int kWave = 64;
+constexpr int kGroup = 128;  // K-block / scale group width
+
+// ---------------------------------------------------------------------------
+// buffer resources and direct global->LDS loads
+// ---------------------------------------------------------------------------
+extern "C" __device__ void hk_raw_buffer_load_lds(i32x4 rsrc, HK_LDS uint32_t* lds_base, int size,
+                                                  int voffset, int soffset, int offset,
+                                                  int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+// 128-bit buffer descriptor: base address, stride 0, num_records = bytes that
+// may be read (offsets past it read as zero), raw untyped dword access.
+__device__ __forceinline__ i32x4 make_srd(const void* base, uint32_t num_bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(p & 0xffffffffu));
+  r.y = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(p >> 32));
+  r.z = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(num_bytes));
+  r.w = 0x00020000;
+  return r;
+}
+
+// One wave instruction: lane i copies 16 bytes from rsrc+voffset into
+// lds_base + 16*i (lds_base must be wave-uniform).
+__device__ __forceinline__ void load_lds_16B(i32x4 rsrc, void* lds_base, int voffset) {
+  hk_raw_buffer_load_lds(rsrc, reinterpret_cast<HK_LDS uint32_t*>(
+                                   reinterpret_cast<uintptr_t>(lds_base)),
+                         16, voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ---------------------------------------------------------------------------
+// MFMA: D(16x16 fp32) += A(16x128 e4m3) . B(16x128 e4m3)^T
+// Lane l supplies row (l % 16) of each operand and 32 bytes of its K range;
+// both operands use the same lane->K assignment, so any bijection of the 128
+// K bytes onto (l / 16, byte) gives the full dot product.  Output: lane l holds
+// D[4*(l/16) + r][l % 16], r = 0..3.  Zero scale operands select the unscaled
+// instruction (v_mfma_f32_16x16x128_f8f6f4).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma_e4m3_16x16x128(const i32x8& a, const i32x8& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// number formats
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t f32_bits(float x) { return __float_as_uint(x); }
+
+// fp32 -> bf16 bits, round to nearest even.
+__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
+  const uint32_t u = f32_bits(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // NaN stays NaN
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return bf16_rne_bits(lo) | (bf16_rne_bits(hi) << 16);
+}
+
+// fp32 -> OCP e4m3fn byte: round to nearest even, saturate to +-448,
+// NaN -> 0x7f | sign.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  const uint32_t u = f32_bits(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  const float af = __uint_as_float(a);
+  if (af >= 448.0f) return sign | 0x7eu;
+  if (af < 0.015625f) {  // below 2^-6: subnormal grid of step 2^-9
+    const float m = __builtin_rintf(af * 512.0f);  // exact scaling, RNE
+    return sign | static_cast<uint32_t>(m);       // m == 8 encodes 2^-6
+  }
+  // normal: keep 3 mantissa bits with RNE on the 20 dropped bits
+  const uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;
+  return sign | (r - (120u << 3));  // rebias exponent 127 -> 7
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t q) {
+  const uint32_t s = (q & 0x80u) << 24;
+  const uint32_t e = (q >> 3) & 0xfu;
+  const uint32_t m = q & 0x7u;
+  float v;
+  if (e == 0)
+    v = static_cast<float>(m) * 0.001953125f;  // m * 2^-9
+  else if (e == 0xf && m == 0x7)
+    v = __uint_as_float(0x7fc00000u);
+  else
+    v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return __uint_as_float(__float_as_uint(v) | s);
+}
+
+__device__ __forceinline__ float scale_from_amax(float amax) {
+  return amax > 0.0f ? amax / 448.0f : 1.0f;
+}
+
+// ---------------------------------------------------------------------------
+// wave reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+}  // namespace hkmoe

@@ -1,0 +1,415 @@
+// Routing, scatter (permute), requantisation, combine and quantiser kernels
+// for the gfx950 FP8 MoE path.  These are HBM/latency-bound integer and byte
+// kernels: 16-byte coalesced accesses, LDS counters, wave-level ballots and
+// shuffles -- no matrix cores.
+//
+// The reference contains none of these operations (no router, histogram,
+// permutation or combine exists under /root/reference); their semantics are
+// the path's frozen specification, restated on the CPU in oracle/spec.py.
+#pragma once
+
+#include "common.hpp"
+
+namespace hkmoe {
+
+constexpr int kRouteTok = 32;      // tokens per routing/scatter workgroup
+constexpr int kRouteThreads = 256; // 4 waves, 8 tokens each
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopK = 32;
+constexpr int kScanThreads = 1024;
+
+__device__ __forceinline__ bool route_better(float av, int ai, float bv, int bi) {
+  if (bi < 0) return ai >= 0;
+  if (ai < 0) return false;
+  return av > bv || (av == bv && ai < bi);
+}
+
+// ---------------------------------------------------------------------------
+// 1. top-k + softmax + per-block histogram.  One wave per token.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kRouteThreads) void route_topk_kernel(
+    const float* __restrict__ logits, int num_tokens, int num_experts, int top_k,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w, int32_t* __restrict__ block_counts) {
+  __shared__ int hist[kMaxExperts];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int e = threadIdx.x; e < num_experts; e += kRouteThreads) hist[e] = 0;
+  __syncthreads();
+
+  const int chunks = (num_experts + 63) >> 6;
+  const int t0 = blockIdx.x * kRouteTok;
+  for (int tt = wave; tt < kRouteTok; tt += kRouteThreads / 64) {
+    const int t = t0 + tt;
+    if (t >= num_tokens) break;
+    const float* row = logits + static_cast<int64_t>(t) * num_experts;
+    float v[kMaxExperts / 64];
+#pragma unroll
+    for (int c = 0; c < kMaxExperts / 64; ++c) {
+      const int id = c * 64 + lane;
+      v[c] = (c < chunks && id < num_experts) ? row[id] : 0.0f;
+    }
+    uint32_t taken = 0;
+    float my_v = 0.0f, v0 = 0.0f;
+    int my_id = 0;
+    for (int j = 0; j < top_k; ++j) {
+      float bv = 0.0f;
+      int bi = -1;
+#pragma unroll
+      for (int c = 0; c < kMaxExperts / 64; ++c) {
+        const int id = c * 64 + lane;
+        if (c < chunks && id < num_experts && !((taken >> c) & 1u) && route_better(v[c], id, bv, bi)) {
+          bv = v[c];
+          bi = id;
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (route_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+      }
+      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+      if (j == 0) v0 = bv;
+      if (lane == j) { my_v = bv; my_id = bi; }
+    }
+    const float ex = (lane < top_k) ? expf(my_v - v0) : 0.0f;
+    float tot = 0.0f;
+    for (int j = 0; j < top_k; ++j) tot = tot + __shfl(ex, j, 64);
+    if (lane < top_k) {
+      topk_idx[static_cast<int64_t>(t) * top_k + lane] = my_id;
+      topk_w[static_cast<int64_t>(t) * top_k + lane] = ex / tot;
+      atomicAdd(&hist[my_id], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < num_experts; e += kRouteThreads)
+    block_counts[static_cast<int64_t>(blockIdx.x) * num_experts + e] = hist[e];
+}
+
+// ---------------------------------------------------------------------------
+// 2. offsets: per-expert exclusive scan over blocks, then over experts.
+//    One workgroup of 1024 threads; thread = (part, expert).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += n;
+  }
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    const int nw = blockDim.x >> 6;
+    int wv = lane < nw ? wave_tot[lane] : 0;
+    int wi = wv;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int n = __shfl_up(wi, o, 64);
+      if (lane >= o) wi += n;
+    }
+    if (lane < nw) wave_tot[lane] = wi - wv;
+  }
+  __syncthreads();
+  const int r = wave_tot[wave] + incl - v;
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
+    const int32_t* __restrict__ block_counts, int nblk, int num_experts, int e_stride, int parts,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ block_base,
+    int32_t* __restrict__ mtile_offsets, int tile_m, float* amax_reset) {
+  __shared__ int part_sum[kScanThreads];
+  __shared__ int wave_tot[kScanThreads / 64];
+  const int tid = threadIdx.x;
+  const int e = tid % e_stride;
+  const int part = tid / e_stride;
+  const int per = (nblk + parts - 1) / parts;
+  const int b0 = part * per, b1 = min(nblk, b0 + per);
+  const bool act = (e < num_experts) && (part < parts);
+
+  int s = 0;
+  if (act) {
+    for (int b = b0; b < b1; b += 16) {
+      int c[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        c[u] = (b + u < b1) ? block_counts[static_cast<int64_t>(b + u) * num_experts + e] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += c[u];
+    }
+  }
+  part_sum[tid] = act ? s : 0;
+  __syncthreads();
+  // prefix over parts for this expert, and the expert total
+  int before = 0, total = 0;
+  if (e < num_experts) {
+    for (int q = 0; q < parts; ++q) {
+      const int v = part_sum[q * e_stride + e];
+      if (q < part) before += v;
+      total += v;
+    }
+  }
+  if (act) {
+    int run = before;
+    for (int b = b0; b < b1; ++b) {
+      const int64_t i = static_cast<int64_t>(b) * num_experts + e;
+      const int c = block_counts[i];
+      block_base[i] = run;
+      run += c;
+    }
+  }
+  // scan over experts (threads with part == 0 carry the expert totals)
+  const int cnt = (part == 0 && e < num_experts) ? total : 0;
+  const int mt = (cnt + tile_m - 1) / tile_m;
+  const int off = block_exclusive_scan(cnt, wave_tot);
+  const int moff = block_exclusive_scan(mt, wave_tot);
+  if (part == 0 && e < num_experts) {
+    counts[e] = cnt;
+    offsets[e] = off;
+    mtile_offsets[e] = moff;
+    if (e == num_experts - 1) {
+      offsets[num_experts] = off + cnt;
+      mtile_offsets[num_experts] = moff + mt;
+    }
+  }
+  if (tid == 0 && amax_reset != nullptr) *amax_reset = 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// 3. stable scatter + row gather.  Same token chunks as route_topk_kernel.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kRouteThreads) void scatter_kernel(
+    const int32_t* __restrict__ topk_idx, int num_tokens, int num_experts, int top_k,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ block_base,
+    int32_t* __restrict__ perm, int32_t* __restrict__ inv_perm, const uint8_t* __restrict__ x_q,
+    const float* __restrict__ x_scale, int64_t hidden, int block_scaled, uint8_t* __restrict__ xp,
+    float* __restrict__ xps_t, int64_t rows_total) {
+  __shared__ int ctr[kMaxExperts];
+  __shared__ int pos[kRouteTok * kMaxTopK];
+  const int lane = threadIdx.x & 63;
+  const int t0 = blockIdx.x * kRouteTok;
+  const int ntok = min(kRouteTok, num_tokens - t0);
+  const int nslot = ntok * top_k;
+  const int64_t f0 = static_cast<int64_t>(t0) * top_k;
+  for (int e = threadIdx.x; e < num_experts; e += kRouteThreads)
+    ctr[e] = offsets[e] + block_base[static_cast<int64_t>(blockIdx.x) * num_experts + e];
+  __syncthreads();
+
+  if (threadIdx.x < 64) {
+    int nbits = 0;
+    while ((1 << nbits) < num_experts) ++nbits;
+    for (int s0 = 0; s0 < nslot; s0 += 64) {
+      const int s = s0 + lane;
+      const bool valid = s < nslot;
+      const int e = valid ? topk_idx[f0 + s] : 0;
+      uint64_t peers = __ballot(valid);
+      for (int b = 0; b < nbits; ++b) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t bal = __ballot(bit);
+        peers &= bit ? bal : ~bal;
+      }
+      const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+      const int rank = __popcll(peers & lt);
+      const int leader = valid ? (__ffsll(static_cast<long long>(peers)) - 1) : 0;
+      int base = 0;
+      if (valid && lane == leader) base = atomicAdd(&ctr[e], __popcll(peers));
+      base = __shfl(base, leader, 64);
+      if (valid) {
+        const int p = base + rank;
+        perm[p] = static_cast<int32_t>(f0 + s);
+        inv_perm[f0 + s] = p;
+        pos[s] = p;
+      }
+    }
+  }
+  __syncthreads();
+  if (x_q == nullptr) return;
+
+  // gather: each token row is read once and written to its top_k destinations
+  const int64_t chunks = hidden / 16;
+  const int64_t work = static_cast<int64_t>(ntok) * chunks;
+  for (int64_t w = threadIdx.x; w < work; w += kRouteThreads) {
+    const int tt = static_cast<int>(w / chunks);
+    const int64_t c = w - static_cast<int64_t>(tt) * chunks;
+    const uint4 v = *reinterpret_cast<const uint4*>(x_q + static_cast<int64_t>(t0 + tt) * hidden + c * 16);
+    for (int j = 0; j < top_k; ++j) {
+      const int p = pos[tt * top_k + j];
+      *reinterpret_cast<uint4*>(xp + static_cast<int64_t>(p) * hidden + c * 16) = v;
+    }
+  }
+  if (block_scaled) {
+    const int groups = static_cast<int>(hidden / kGroup);
+    const int swork = ntok * groups;
+    for (int w = threadIdx.x; w < swork; w += kRouteThreads) {
+      const int tt = w / groups, g = w - tt * groups;
+      const float sv = x_scale[static_cast<int64_t>(t0 + tt) * groups + g];
+      for (int j = 0; j < top_k; ++j)
+        xps_t[static_cast<int64_t>(g) * rows_total + pos[tt * top_k + j]] = sv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. requantisation of the bf16 intermediate
+// ---------------------------------------------------------------------------
+// 1x128 groups: one workgroup (256 threads) per row, one wave per group.
+__global__ __launch_bounds__(256) void requant_group_kernel(const uint16_t* __restrict__ h,
+                                                            int64_t rows, int inter,
+                                                            uint8_t* __restrict__ hq,
+                                                            float* __restrict__ hs_t) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = blockIdx.x;
+  const int groups = inter / kGroup;
+  for (int g = wave; g < groups; g += 4) {
+    const int64_t base = r * inter + g * kGroup + lane * 2;
+    const uint32_t pair = *reinterpret_cast<const uint32_t*>(h + base);
+    const float a = bf16_bits_to_f32(pair & 0xffffu), b = bf16_bits_to_f32(pair >> 16);
+    const float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
+    const float s = scale_from_amax(amax);
+    const uint32_t q = f32_to_e4m3(a / s) | (f32_to_e4m3(b / s) << 8);
+    *reinterpret_cast<uint16_t*>(hq + base) = static_cast<uint16_t>(q);
+    if (lane == 0) hs_t[static_cast<int64_t>(g) * rows + r] = s;
+  }
+}
+
+// per-tensor: amax was accumulated by GEMM 1; 8 elements per thread.
+__global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __restrict__ h,
+                                                             int64_t n8, const float* amax,
+                                                             uint8_t* __restrict__ hq,
+                                                             float* __restrict__ hs) {
+  const float s = scale_from_amax(*amax);
+  if (blockIdx.x == 0 && threadIdx.x == 0) hs[0] = s;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n8; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const uint4 v = reinterpret_cast<const uint4*>(h)[i];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint2 o;
+    uint32_t* op = &o.x;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t pr = w[q * 2 + u];
+        acc |= f32_to_e4m3(bf16_bits_to_f32(pr & 0xffffu) / s) << (16 * u);
+        acc |= f32_to_e4m3(bf16_bits_to_f32(pr >> 16) / s) << (16 * u + 8);
+      }
+      op[q] = acc;
+    }
+    reinterpret_cast<uint2*>(hq)[i] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 5. combine: out[t] = bf16(sum_j w[t,j] * y[inv_perm[t*k+j]]), one
+//    workgroup per token, 8 columns (16 bytes) per thread and step.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
+                                                      const float* __restrict__ topk_w,
+                                                      const int32_t* __restrict__ inv_perm,
+                                                      int top_k, int hidden,
+                                                      uint16_t* __restrict__ out) {
+  const int64_t t = blockIdx.x;
+  const int cols8 = hidden / 8;
+  for (int c = threadIdx.x; c < cols8; c += 256) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < top_k; ++j) {
+      const int64_t f = t * top_k + j;
+      const float w = topk_w[f];
+      const int64_t p = inv_perm[f];
+      const uint4 v = *reinterpret_cast<const uint4*>(y + p * hidden + c * 8);
+      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc[2 * u] = acc[2 * u] + w * bf16_bits_to_f32(wv[u] & 0xffffu);
+        acc[2 * u + 1] = acc[2 * u + 1] + w * bf16_bits_to_f32(wv[u] >> 16);
+      }
+    }
+    uint4 o;
+    o.x = pack_bf16x2(acc[0], acc[1]);
+    o.y = pack_bf16x2(acc[2], acc[3]);
+    o.z = pack_bf16x2(acc[4], acc[5]);
+    o.w = pack_bf16x2(acc[6], acc[7]);
+    *reinterpret_cast<uint4*>(out + t * hidden + c * 8) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 6. quantisers (fp32 input) used to build e4m3 operands on the device
+// ---------------------------------------------------------------------------
+// 1x128 groups, row-major scales [R, C/128]; one wave per group.
+__global__ __launch_bounds__(256) void quant_group_kernel(const float* __restrict__ x, int64_t rows,
+                                                          int64_t cols, uint8_t* __restrict__ q,
+                                                          float* __restrict__ s) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gid = blockIdx.x * 4ll + (threadIdx.x >> 6);
+  const int64_t groups = cols / kGroup;
+  if (gid >= rows * groups) return;
+  const int64_t r = gid / groups, g = gid - r * groups;
+  const int64_t base = r * cols + g * kGroup + lane * 2;
+  const float2 v = *reinterpret_cast<const float2*>(x + base);
+  const float amax = wave_max(fmaxf(fabsf(v.x), fabsf(v.y)));
+  const float sc = scale_from_amax(amax);
+  const uint32_t qq = f32_to_e4m3(v.x / sc) | (f32_to_e4m3(v.y / sc) << 8);
+  *reinterpret_cast<uint16_t*>(q + base) = static_cast<uint16_t>(qq);
+  if (lane == 0) s[gid] = sc;
+}
+
+// 128x128 blocks of [B, R, C]; one workgroup (256 threads) per block.
+__global__ __launch_bounds__(256) void quant_block_kernel(const float* __restrict__ x, int64_t rows,
+                                                          int64_t cols, uint8_t* __restrict__ q,
+                                                          float* __restrict__ s) {
+  __shared__ float red[4];
+  const int64_t bc = cols / kGroup, br = rows / kGroup;
+  const int64_t blk = blockIdx.x;
+  const int64_t b = blk / (br * bc);
+  const int64_t rem = blk - b * br * bc;
+  const int64_t bi = rem / bc, bj = rem - bi * bc;
+  const float* xb = x + (b * rows + bi * kGroup) * cols + bj * kGroup;
+  uint8_t* qb = q + (b * rows + bi * kGroup) * cols + bj * kGroup;
+  // thread: rows (tid/32) + 8*u, columns 4*(tid%32) .. +3
+  const int cr = threadIdx.x >> 5, cc = (threadIdx.x & 31) * 4;
+  float m = 0.0f;
+  for (int u = 0; u < 16; ++u) {
+    const float4 v = *reinterpret_cast<const float4*>(xb + static_cast<int64_t>(cr + 8 * u) * cols + cc);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = scale_from_amax(amax);
+  for (int u = 0; u < 16; ++u) {
+    const int64_t off = static_cast<int64_t>(cr + 8 * u) * cols + cc;
+    const float4 v = *reinterpret_cast<const float4*>(xb + off);
+    const uint32_t qq = f32_to_e4m3(v.x / sc) | (f32_to_e4m3(v.y / sc) << 8) |
+                        (f32_to_e4m3(v.z / sc) << 16) | (f32_to_e4m3(v.w / sc) << 24);
+    *reinterpret_cast<uint32_t*>(qb + off) = qq;
+  }
+  if (threadIdx.x == 0) s[blk] = sc;
+}
+
+__global__ __launch_bounds__(256) void amax_kernel(const float* __restrict__ x, int64_t n,
+                                                   float* amax) {
+  float m = 0.0f;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    m = fmaxf(m, fabsf(x[i]));
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) atomicMax(reinterpret_cast<unsigned int*>(amax), __float_as_uint(m));
+}
+
+__global__ void fill_f32_kernel(float* p, float v) { *p = v; }
+
+__global__ __launch_bounds__(256) void quant_tensor_kernel(const float* __restrict__ x, int64_t n,
+                                                           const float* amax,
+                                                           uint8_t* __restrict__ q,
+                                                           float* __restrict__ s) {
+  const float sc = scale_from_amax(*amax);
+  if (blockIdx.x == 0 && threadIdx.x == 0) s[0] = sc;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    q[i] = static_cast<uint8_t>(f32_to_e4m3(x[i] / sc));
+}
+
+}  // namespace hkmoe

@@ -1,0 +1,389 @@
+// pybind11 module `tk_kernel`: the Python-callable dispatch_* entry points of
+// the FP8 MoE path, layered over the C ABI in include/hkmoe.h.
+//
+// Mirrors the reference's binding convention (include/pyutils/pyutils.cuh):
+// positional torch.Tensor arguments, each checked to be a Tensor
+// (class-name check), contiguous and not on the CPU (pyutils.cuh:17-26), with
+// failures raised as RuntimeError; `dispatch_micro(A, B, C)` keeps the
+// reference's dense-GEMM call (kernels/cdna3/gemm/fp8fp32/mi300x/
+// 8192_256_256_64_32/data_logs/0613_003858_outputs/256_256_64_32.cpp:202-212).
+// Additions over the reference: dtype and shape checks, and launches go to
+// torch's current stream of the current device instead of the null stream.
+//
+// No torch C++ headers: tensors are read through their Python attributes, so
+// this module only depends on pybind11 and the C ABI.
+#include <pybind11/pybind11.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/hkmoe.h"
+
+namespace py = pybind11;
+
+namespace {
+
+struct TensorArg {
+  void* ptr = nullptr;
+  std::vector<int64_t> shape;
+  std::string dtype;
+  int64_t numel() const {
+    int64_t n = 1;
+    for (auto s : shape) n *= s;
+    return n;
+  }
+};
+
+TensorArg as_tensor(const py::object& obj, const char* name) {
+  if (!py::hasattr(obj, "__class__") ||
+      obj.attr("__class__").attr("__name__").cast<std::string>() != "Tensor")
+    throw std::runtime_error(std::string(name) + ": expected a torch.Tensor");
+  if (!obj.attr("is_contiguous")().cast<bool>())
+    throw std::runtime_error(std::string(name) + ": tensor must be contiguous");
+  if (obj.attr("device").attr("type").cast<std::string>() == "cpu")
+    throw std::runtime_error(std::string(name) + ": tensor must be on a GPU device");
+  TensorArg t;
+  t.ptr = reinterpret_cast<void*>(obj.attr("data_ptr")().cast<uintptr_t>());
+  for (auto s : obj.attr("shape").cast<py::tuple>()) t.shape.push_back(s.cast<int64_t>());
+  t.dtype = py::str(obj.attr("dtype")).cast<std::string>();
+  return t;
+}
+
+TensorArg as_tensor_opt(const py::object& obj, const char* name) {
+  if (obj.is_none()) return TensorArg{};
+  return as_tensor(obj, name);
+}
+
+void want_dtype(const TensorArg& t, const char* name, const char* dtype) {
+  if (t.ptr != nullptr && t.dtype != dtype)
+    throw std::runtime_error(std::string(name) + ": expected dtype " + dtype + ", got " + t.dtype);
+}
+
+void want_dim(const TensorArg& t, const char* name, size_t nd) {
+  if (t.shape.size() != nd)
+    throw std::runtime_error(std::string(name) + ": expected " + std::to_string(nd) + "-D tensor");
+}
+
+hkmoe_stream_t current_stream() {
+  // Intentionally leaked: a static py::object would be destroyed after the
+  // interpreter has finalised and crash the process at exit.
+  static py::object* torch_cuda = new py::object(py::module_::import("torch").attr("cuda"));
+  const uintptr_t s = torch_cuda->attr("current_stream")().attr("cuda_stream").cast<uintptr_t>();
+  return reinterpret_cast<hkmoe_stream_t>(s);
+}
+
+void check(int rc) {
+  if (rc != HKMOE_OK) throw std::runtime_error(std::string("hkmoe: ") + hkmoe_last_error());
+}
+
+constexpr const char* kF8 = "torch.float8_e4m3fn";
+constexpr const char* kBf16 = "torch.bfloat16";
+constexpr const char* kF32 = "torch.float32";
+constexpr const char* kI32 = "torch.int32";
+
+int scale_mode_of(const TensorArg& s) {
+  return (s.shape.size() <= 1 && s.numel() == 1) ? HKMOE_SCALE_TENSOR : HKMOE_SCALE_BLOCK;
+}
+
+// ---------------------------------------------------------------------------
+
+void dispatch_gemm(py::object A, py::object B, py::object C, py::object sa, py::object sb) {
+  auto a = as_tensor(A, "A"), b = as_tensor(B, "B"), c = as_tensor(C, "C");
+  auto as = as_tensor_opt(sa, "scale_a"), bs = as_tensor_opt(sb, "scale_b");
+  want_dtype(a, "A", kF8);
+  want_dtype(b, "B", kF8);
+  want_dtype(as, "scale_a", kF32);
+  want_dtype(bs, "scale_b", kF32);
+  // Like gl<> views (pyutils.cuh:28-38), leading size-1 dims are ignored.
+  auto rows_cols = [](const TensorArg& t, const char* n) {
+    if (t.shape.size() < 2 || t.shape.size() > 4) throw std::runtime_error(std::string(n) + ": expected 2-4 dims");
+    for (size_t i = 0; i + 2 < t.shape.size(); ++i)
+      if (t.shape[i] != 1) throw std::runtime_error(std::string(n) + ": leading dims must be 1");
+    return std::pair<int64_t, int64_t>(t.shape[t.shape.size() - 2], t.shape.back());
+  };
+  auto [m, k] = rows_cols(a, "A");
+  auto [n, kb] = rows_cols(b, "B");
+  auto [cm, cn] = rows_cols(c, "C");
+  if (k != kb) throw std::runtime_error("A and B must have the same K");
+  if (cm != m || cn != n) throw std::runtime_error("C must be [M, N]");
+  if (as.ptr && as.numel() != 1) throw std::runtime_error("scale_a must hold one value");
+  if (bs.ptr && bs.numel() != 1) throw std::runtime_error("scale_b must hold one value");
+  int out;
+  if (c.dtype == kBf16) out = HKMOE_BF16;
+  else if (c.dtype == kF32) out = HKMOE_F32;
+  else throw std::runtime_error("C: expected bfloat16 or float32");
+  check(hkmoe_gemm_fp8(a.ptr, b.ptr, c.ptr, m, n, k, static_cast<const float*>(as.ptr),
+                       static_cast<const float*>(bs.ptr), out, current_stream()));
+}
+
+void dispatch_micro(py::object A, py::object B, py::object C) {
+  dispatch_gemm(A, B, C, py::none(), py::none());
+}
+
+void dispatch_route_topk(py::object logits, py::object idx, py::object w, py::object bc) {
+  auto l = as_tensor(logits, "logits"), i = as_tensor(idx, "topk_idx"), ww = as_tensor(w, "topk_w"),
+       b = as_tensor(bc, "block_counts");
+  want_dtype(l, "logits", kF32);
+  want_dtype(i, "topk_idx", kI32);
+  want_dtype(ww, "topk_w", kF32);
+  want_dtype(b, "block_counts", kI32);
+  want_dim(l, "logits", 2);
+  want_dim(i, "topk_idx", 2);
+  const int64_t t = l.shape[0], e = l.shape[1], k = i.shape[1];
+  if (i.shape[0] != t || ww.shape != i.shape) throw std::runtime_error("topk_idx/topk_w must be [T, k]");
+  if (b.numel() < static_cast<int64_t>(hkmoe_route_blocks(t)) * e)
+    throw std::runtime_error("block_counts too small: need route_blocks(T) * E");
+  check(hkmoe_route_topk(static_cast<const float*>(l.ptr), t, static_cast<int32_t>(e),
+                         static_cast<int32_t>(k), static_cast<int32_t*>(i.ptr),
+                         static_cast<float*>(ww.ptr), static_cast<int32_t*>(b.ptr), current_stream()));
+}
+
+void dispatch_expert_offsets(py::object bc, int64_t num_tokens, py::object counts, py::object offsets,
+                             py::object block_base, py::object mtile_offsets, py::object amax) {
+  auto b = as_tensor(bc, "block_counts"), c = as_tensor(counts, "counts"),
+       o = as_tensor(offsets, "offsets"), bb = as_tensor(block_base, "block_base"),
+       mo = as_tensor(mtile_offsets, "mtile_offsets"), am = as_tensor_opt(amax, "amax");
+  for (auto* t : {&b, &c, &o, &bb, &mo}) want_dtype(*t, "int tensor", kI32);
+  want_dtype(am, "amax", kF32);
+  const int64_t e = c.numel();
+  if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
+  if (b.numel() < static_cast<int64_t>(hkmoe_route_blocks(num_tokens)) * e || bb.numel() < b.numel())
+    throw std::runtime_error("block_counts/block_base too small");
+  check(hkmoe_expert_offsets(static_cast<const int32_t*>(b.ptr), num_tokens, static_cast<int32_t>(e),
+                             static_cast<int32_t*>(c.ptr), static_cast<int32_t*>(o.ptr),
+                             static_cast<int32_t*>(bb.ptr), static_cast<int32_t*>(mo.ptr),
+                             static_cast<float*>(am.ptr), current_stream()));
+}
+
+void dispatch_scatter(py::object idx, py::object offsets, py::object block_base, py::object perm,
+                      py::object inv_perm, py::object x_q, py::object x_scale, py::object xp,
+                      py::object xps_t) {
+  auto i = as_tensor(idx, "topk_idx"), o = as_tensor(offsets, "offsets"),
+       bb = as_tensor(block_base, "block_base"), p = as_tensor(perm, "perm"),
+       ip = as_tensor(inv_perm, "inv_perm"), x = as_tensor_opt(x_q, "x_q"),
+       xs = as_tensor_opt(x_scale, "x_scale"), d = as_tensor_opt(xp, "xp"),
+       ds = as_tensor_opt(xps_t, "xp_scale_t");
+  want_dim(i, "topk_idx", 2);
+  for (auto* t : {&i, &o, &bb, &p, &ip}) want_dtype(*t, "int tensor", kI32);
+  want_dtype(x, "x_q", kF8);
+  want_dtype(d, "xp", kF8);
+  want_dtype(xs, "x_scale", kF32);
+  want_dtype(ds, "xp_scale_t", kF32);
+  const int64_t t = i.shape[0], k = i.shape[1], e = o.numel() - 1;
+  if (p.numel() != t * k || ip.numel() != t * k) throw std::runtime_error("perm/inv_perm must hold T*k values");
+  int64_t hidden = 0;
+  int mode = HKMOE_SCALE_TENSOR;
+  if (x.ptr) {
+    want_dim(x, "x_q", 2);
+    hidden = x.shape[1];
+    if (x.shape[0] != t) throw std::runtime_error("x_q must be [T, H]");
+    if (!d.ptr || d.numel() != t * k * hidden) throw std::runtime_error("xp must be [T*k, H]");
+    if (ds.ptr) {
+      mode = HKMOE_SCALE_BLOCK;
+      if (!xs.ptr || xs.numel() != t * (hidden / 128) || ds.numel() != t * k * (hidden / 128))
+        throw std::runtime_error("block scales: x_scale [T, H/128], xp_scale_t [H/128, T*k]");
+    }
+  }
+  check(hkmoe_scatter(static_cast<const int32_t*>(i.ptr), t, static_cast<int32_t>(e),
+                      static_cast<int32_t>(k), static_cast<const int32_t*>(o.ptr),
+                      static_cast<const int32_t*>(bb.ptr), static_cast<int32_t*>(p.ptr),
+                      static_cast<int32_t*>(ip.ptr), x.ptr, static_cast<const float*>(xs.ptr), hidden,
+                      mode, d.ptr, static_cast<float*>(ds.ptr), current_stream()));
+}
+
+void dispatch_grouped_gemm1(py::object xp, py::object xps, py::object w13, py::object w13s,
+                            py::object offsets, py::object mtile_offsets, py::object h, py::object amax) {
+  auto x = as_tensor(xp, "xp"), xs = as_tensor(xps, "xp_scale"), w = as_tensor(w13, "w13"),
+       ws = as_tensor(w13s, "w13_scale"), o = as_tensor(offsets, "offsets"),
+       mo = as_tensor(mtile_offsets, "mtile_offsets"), hh = as_tensor(h, "h"),
+       am = as_tensor_opt(amax, "amax");
+  want_dtype(x, "xp", kF8);
+  want_dtype(w, "w13", kF8);
+  want_dtype(xs, "xp_scale", kF32);
+  want_dtype(ws, "w13_scale", kF32);
+  want_dtype(hh, "h", kBf16);
+  want_dtype(am, "amax", kF32);
+  want_dim(x, "xp", 2);
+  want_dim(w, "w13", 3);
+  const int64_t rows = x.shape[0], hidden = x.shape[1], e = w.shape[0], inter = w.shape[1] / 2;
+  if (w.shape[2] != hidden || w.shape[1] % 2) throw std::runtime_error("w13 must be [E, 2I, H]");
+  if (hh.numel() != rows * inter) throw std::runtime_error("h must be [rows, I]");
+  if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
+  const int mode = scale_mode_of(xs);
+  if (mode == HKMOE_SCALE_TENSOR && ws.numel() != e) throw std::runtime_error("w13_scale must be [E]");
+  if (mode == HKMOE_SCALE_BLOCK &&
+      (xs.numel() != rows * (hidden / 128) || ws.numel() != e * (2 * inter / 128) * (hidden / 128)))
+    throw std::runtime_error("block scales: xp_scale_t [H/128, rows], w13_scale [E, 2I/128, H/128]");
+  check(hkmoe_grouped_gemm1(x.ptr, static_cast<const float*>(xs.ptr), w.ptr,
+                            static_cast<const float*>(ws.ptr), static_cast<const int32_t*>(o.ptr),
+                            static_cast<const int32_t*>(mo.ptr), rows, static_cast<int32_t>(e),
+                            static_cast<int32_t>(hidden), static_cast<int32_t>(inter), mode, hh.ptr,
+                            static_cast<float*>(am.ptr), current_stream()));
+}
+
+void dispatch_requant(py::object h, py::object amax, py::object hq, py::object hs) {
+  auto hh = as_tensor(h, "h"), am = as_tensor_opt(amax, "amax"), q = as_tensor(hq, "hq"),
+       s = as_tensor(hs, "hs");
+  want_dtype(hh, "h", kBf16);
+  want_dtype(q, "hq", kF8);
+  want_dtype(s, "hs", kF32);
+  want_dtype(am, "amax", kF32);
+  want_dim(hh, "h", 2);
+  const int64_t rows = hh.shape[0], inter = hh.shape[1];
+  if (q.numel() != rows * inter) throw std::runtime_error("hq must be [rows, I]");
+  // per-tensor mode iff GEMM 1's running amax is supplied
+  const int mode = am.ptr ? HKMOE_SCALE_TENSOR : HKMOE_SCALE_BLOCK;
+  if (mode == HKMOE_SCALE_TENSOR && s.numel() != 1) throw std::runtime_error("hs must hold one value");
+  if (mode == HKMOE_SCALE_BLOCK && s.numel() != rows * (inter / 128))
+    throw std::runtime_error("hs must be [I/128, rows] for group scales");
+  check(hkmoe_requant(hh.ptr, rows, static_cast<int32_t>(inter), mode, static_cast<const float*>(am.ptr),
+                      q.ptr, static_cast<float*>(s.ptr), current_stream()));
+}
+
+void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::object w2s,
+                            py::object offsets, py::object mtile_offsets, py::object y) {
+  auto q = as_tensor(hq, "hq"), s = as_tensor(hs, "hs"), w = as_tensor(w2, "w2"),
+       ws = as_tensor(w2s, "w2_scale"), o = as_tensor(offsets, "offsets"),
+       mo = as_tensor(mtile_offsets, "mtile_offsets"), yy = as_tensor(y, "y");
+  want_dtype(q, "hq", kF8);
+  want_dtype(w, "w2", kF8);
+  want_dtype(s, "hs", kF32);
+  want_dtype(ws, "w2_scale", kF32);
+  want_dtype(yy, "y", kBf16);
+  want_dim(q, "hq", 2);
+  want_dim(w, "w2", 3);
+  const int64_t rows = q.shape[0], inter = q.shape[1], e = w.shape[0], hidden = w.shape[1];
+  if (w.shape[2] != inter) throw std::runtime_error("w2 must be [E, H, I]");
+  if (yy.numel() != rows * hidden) throw std::runtime_error("y must be [rows, H]");
+  if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
+  const int mode = scale_mode_of(s);
+  if (mode == HKMOE_SCALE_TENSOR && ws.numel() != e) throw std::runtime_error("w2_scale must be [E]");
+  if (mode == HKMOE_SCALE_BLOCK &&
+      (s.numel() != rows * (inter / 128) || ws.numel() != e * (hidden / 128) * (inter / 128)))
+    throw std::runtime_error("block scales: hs [I/128, rows], w2_scale [E, H/128, I/128]");
+  check(hkmoe_grouped_gemm2(q.ptr, static_cast<const float*>(s.ptr), w.ptr,
+                            static_cast<const float*>(ws.ptr), static_cast<const int32_t*>(o.ptr),
+                            static_cast<const int32_t*>(mo.ptr), rows, static_cast<int32_t>(e),
+                            static_cast<int32_t>(hidden), static_cast<int32_t>(inter), mode, yy.ptr,
+                            current_stream()));
+}
+
+void dispatch_combine(py::object y, py::object w, py::object inv_perm, py::object out) {
+  auto yy = as_tensor(y, "y"), ww = as_tensor(w, "topk_w"), ip = as_tensor(inv_perm, "inv_perm"),
+       o = as_tensor(out, "out");
+  want_dtype(yy, "y", kBf16);
+  want_dtype(ww, "topk_w", kF32);
+  want_dtype(ip, "inv_perm", kI32);
+  want_dtype(o, "out", kBf16);
+  want_dim(ww, "topk_w", 2);
+  want_dim(o, "out", 2);
+  const int64_t t = ww.shape[0], k = ww.shape[1], hidden = o.shape[1];
+  if (o.shape[0] != t || yy.numel() != t * k * hidden || ip.numel() != t * k)
+    throw std::runtime_error("combine: y [T*k, H], inv_perm [T*k], out [T, H]");
+  check(hkmoe_combine(yy.ptr, static_cast<const float*>(ww.ptr), static_cast<const int32_t*>(ip.ptr), t,
+                      static_cast<int32_t>(k), static_cast<int32_t>(hidden), o.ptr, current_stream()));
+}
+
+size_t moe_workspace_size(int64_t t, int32_t e, int32_t k, int32_t hidden, int32_t inter, int mode) {
+  return hkmoe_moe_workspace_size(t, e, k, hidden, inter, mode);
+}
+
+void dispatch_moe(py::object x_q, py::object x_scale, py::object logits, py::object w13,
+                  py::object w13s, py::object w2, py::object w2s, int32_t top_k, py::object out,
+                  py::object workspace) {
+  auto x = as_tensor(x_q, "x_q"), xs = as_tensor(x_scale, "x_scale"), l = as_tensor(logits, "logits"),
+       a = as_tensor(w13, "w13"), as = as_tensor(w13s, "w13_scale"), b = as_tensor(w2, "w2"),
+       bs = as_tensor(w2s, "w2_scale"), o = as_tensor(out, "out"), ws = as_tensor(workspace, "workspace");
+  want_dtype(x, "x_q", kF8);
+  want_dtype(a, "w13", kF8);
+  want_dtype(b, "w2", kF8);
+  for (auto* t : {&xs, &l, &as, &bs}) want_dtype(*t, "fp32 tensor", kF32);
+  want_dtype(o, "out", kBf16);
+  want_dim(x, "x_q", 2);
+  want_dim(l, "logits", 2);
+  want_dim(a, "w13", 3);
+  want_dim(b, "w2", 3);
+  const int64_t t = x.shape[0], hidden = x.shape[1], e = a.shape[0], inter = a.shape[1] / 2;
+  if (l.shape[0] != t || l.shape[1] != e) throw std::runtime_error("logits must be [T, E]");
+  if (a.shape[2] != hidden || b.shape[0] != e || b.shape[1] != hidden || b.shape[2] != inter)
+    throw std::runtime_error("w13 must be [E, 2I, H] and w2 [E, H, I]");
+  if (o.numel() != t * hidden) throw std::runtime_error("out must be [T, H]");
+  const int mode = scale_mode_of(xs);
+  if (mode == HKMOE_SCALE_BLOCK &&
+      (xs.numel() != t * (hidden / 128) || as.numel() != e * (2 * inter / 128) * (hidden / 128) ||
+       bs.numel() != e * (hidden / 128) * (inter / 128)))
+    throw std::runtime_error("block scales: x_scale [T, H/128], w13_scale [E, 2I/128, H/128], w2_scale [E, H/128, I/128]");
+  if (mode == HKMOE_SCALE_TENSOR && (as.numel() != e || bs.numel() != e))
+    throw std::runtime_error("per-tensor scales: w13_scale and w2_scale must be [E]");
+  const size_t bytes = static_cast<size_t>(ws.numel()) * (ws.dtype == kF32 || ws.dtype == kI32 ? 4 : 1);
+  check(hkmoe_moe_forward(x.ptr, static_cast<const float*>(xs.ptr), static_cast<const float*>(l.ptr), a.ptr,
+                          static_cast<const float*>(as.ptr), b.ptr, static_cast<const float*>(bs.ptr), t,
+                          static_cast<int32_t>(e), top_k, static_cast<int32_t>(hidden),
+                          static_cast<int32_t>(inter), mode, o.ptr, ws.ptr, bytes, current_stream()));
+}
+
+void dispatch_quant_group(py::object x, py::object q, py::object s) {
+  auto xx = as_tensor(x, "x"), qq = as_tensor(q, "q"), ss = as_tensor(s, "s");
+  want_dtype(xx, "x", kF32);
+  want_dtype(qq, "q", kF8);
+  want_dtype(ss, "s", kF32);
+  want_dim(xx, "x", 2);
+  const int64_t r = xx.shape[0], c = xx.shape[1];
+  if (qq.numel() != r * c || ss.numel() != r * (c / 128)) throw std::runtime_error("quant_group: q [R,C], s [R,C/128]");
+  check(hkmoe_quant_group(static_cast<const float*>(xx.ptr), r, c, qq.ptr, static_cast<float*>(ss.ptr),
+                          current_stream()));
+}
+
+void dispatch_quant_block(py::object x, py::object q, py::object s) {
+  auto xx = as_tensor(x, "x"), qq = as_tensor(q, "q"), ss = as_tensor(s, "s");
+  want_dtype(xx, "x", kF32);
+  want_dtype(qq, "q", kF8);
+  want_dtype(ss, "s", kF32);
+  if (xx.shape.size() != 2 && xx.shape.size() != 3) throw std::runtime_error("quant_block: x must be 2-D or 3-D");
+  const int64_t b = xx.shape.size() == 3 ? xx.shape[0] : 1;
+  const int64_t r = xx.shape[xx.shape.size() - 2], c = xx.shape.back();
+  if (qq.numel() != b * r * c || ss.numel() != b * (r / 128) * (c / 128))
+    throw std::runtime_error("quant_block: q like x, s [B, R/128, C/128]");
+  check(hkmoe_quant_block(static_cast<const float*>(xx.ptr), b, r, c, qq.ptr, static_cast<float*>(ss.ptr),
+                          current_stream()));
+}
+
+void dispatch_quant_tensor(py::object x, py::object q, py::object s, py::object ws) {
+  auto xx = as_tensor(x, "x"), qq = as_tensor(q, "q"), ss = as_tensor(s, "s"), w = as_tensor(ws, "amax_ws");
+  want_dtype(xx, "x", kF32);
+  want_dtype(qq, "q", kF8);
+  want_dtype(ss, "s", kF32);
+  want_dtype(w, "amax_ws", kF32);
+  if (qq.numel() != xx.numel() || ss.numel() != 1 || w.numel() < 1)
+    throw std::runtime_error("quant_tensor: q like x, s [1], amax_ws [1]");
+  check(hkmoe_quant_tensor(static_cast<const float*>(xx.ptr), 1, xx.numel(), qq.ptr,
+                           static_cast<float*>(ss.ptr), static_cast<float*>(w.ptr), current_stream()));
+}
+
+}  // namespace
+
+PYBIND11_MODULE(tk_kernel, m) {
+  m.doc() = "gfx950 FP8 MoE grouped-GEMM path (dispatch_* entry points over the hkmoe C ABI)";
+  m.def("dispatch_micro", &dispatch_micro, "C = A . B^T (e4m3 in, fp32/bf16 out, unit scales)");
+  m.def("dispatch_gemm_fp8", &dispatch_gemm, "C = (sa*sb) A . B^T, per-tensor scales",
+        py::arg("A"), py::arg("B"), py::arg("C"), py::arg("scale_a") = py::none(),
+        py::arg("scale_b") = py::none());
+  m.def("dispatch_route_topk", &dispatch_route_topk);
+  m.def("dispatch_expert_offsets", &dispatch_expert_offsets);
+  m.def("dispatch_scatter", &dispatch_scatter);
+  m.def("dispatch_grouped_gemm1", &dispatch_grouped_gemm1);
+  m.def("dispatch_requant", &dispatch_requant);
+  m.def("dispatch_grouped_gemm2", &dispatch_grouped_gemm2);
+  m.def("dispatch_combine", &dispatch_combine);
+  m.def("dispatch_moe", &dispatch_moe);
+  m.def("dispatch_quant_group", &dispatch_quant_group);
+  m.def("dispatch_quant_block", &dispatch_quant_block);
+  m.def("dispatch_quant_tensor", &dispatch_quant_tensor);
+  m.def("moe_workspace_size", &moe_workspace_size);
+  m.def("route_blocks", [](int64_t t) { return hkmoe_route_blocks(t); });
+  m.def("version", []() { return hkmoe_version(); });
+  m.attr("SCALE_TENSOR") = static_cast<int>(HKMOE_SCALE_TENSOR);
+  m.attr("SCALE_BLOCK") = static_cast<int>(HKMOE_SCALE_BLOCK);
+}

@@ -1,0 +1,152 @@
+"""MoE layer orchestration over the tk_kernel dispatch entry points.
+
+Torch is used only for device memory (allocation of outputs and the
+workspace) and for the current stream; every operation is one of the HIP
+kernels behind ``tk_kernel``.
+"""
+import torch
+
+import tk_kernel
+
+F8 = torch.float8_e4m3fn
+GROUP = 128
+
+
+def _check_dev(*ts):
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("hkmoe: tensors must live on a GPU device")
+
+
+# ----------------------------------------------------------------------------
+# quantisers (device)
+# ----------------------------------------------------------------------------
+def quant_group(x):
+    """fp32 [R, C] -> (e4m3 [R, C], fp32 scales [R, C/128]), 1x128 groups."""
+    _check_dev(x)
+    x = x.float().contiguous()
+    q = torch.empty(x.shape, dtype=F8, device=x.device)
+    s = torch.empty((x.shape[0], x.shape[1] // GROUP), dtype=torch.float32, device=x.device)
+    tk_kernel.dispatch_quant_group(x, q, s)
+    return q, s
+
+
+def quant_block(w):
+    """fp32 [..., R, C] -> (e4m3, fp32 scales [..., R/128, C/128]), 128x128 blocks."""
+    _check_dev(w)
+    w = w.float().contiguous()
+    q = torch.empty(w.shape, dtype=F8, device=w.device)
+    s = torch.empty((*w.shape[:-2], w.shape[-2] // GROUP, w.shape[-1] // GROUP),
+                    dtype=torch.float32, device=w.device)
+    tk_kernel.dispatch_quant_block(w.reshape(-1, w.shape[-2], w.shape[-1]), q, s)
+    return q, s
+
+
+def quant_tensor(x):
+    """fp32 tensor -> (e4m3, fp32 scale [1]), s = amax/448."""
+    _check_dev(x)
+    x = x.float().contiguous()
+    q = torch.empty(x.shape, dtype=F8, device=x.device)
+    s = torch.empty(1, dtype=torch.float32, device=x.device)
+    ws = torch.empty(1, dtype=torch.float32, device=x.device)
+    tk_kernel.dispatch_quant_tensor(x, q, s, ws)
+    return q, s
+
+
+def gemm_fp8(a_q, b_q, scale_a=None, scale_b=None, out_dtype=torch.bfloat16):
+    """C = (sa*sb) A . B^T for e4m3 A [M,K], B [N,K]."""
+    _check_dev(a_q, b_q)
+    c = torch.empty((a_q.shape[0], b_q.shape[0]), dtype=out_dtype, device=a_q.device)
+    tk_kernel.dispatch_gemm_fp8(a_q, b_q, c, scale_a, scale_b)
+    return c
+
+
+# ----------------------------------------------------------------------------
+# the layer
+# ----------------------------------------------------------------------------
+def moe_forward(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k,
+                out=None, workspace=None):
+    """Single-call layer (hkmoe_moe_forward).  Returns the bf16 [T, H] output."""
+    _check_dev(x_q, logits, w13_q, w2_q)
+    t, hidden = x_q.shape
+    e, two_i, _ = w13_q.shape
+    mode = tk_kernel.SCALE_TENSOR if x_scale.numel() == 1 and x_scale.dim() <= 1 else tk_kernel.SCALE_BLOCK
+    if out is None:
+        out = torch.empty((t, hidden), dtype=torch.bfloat16, device=x_q.device)
+    need = tk_kernel.moe_workspace_size(t, e, top_k, hidden, two_i // 2, mode)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x_q.device)
+    tk_kernel.dispatch_moe(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k, out,
+                           workspace)
+    return out
+
+
+def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k):
+    """The layer one kernel at a time; returns a dict of every intermediate."""
+    _check_dev(x_q, logits, w13_q, w2_q)
+    dev = x_q.device
+    t, hidden = x_q.shape
+    e, two_i, _ = w13_q.shape
+    inter = two_i // 2
+    rows = t * top_k
+    block = not (x_scale.numel() == 1 and x_scale.dim() <= 1)
+    i32 = dict(dtype=torch.int32, device=dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    nblk = tk_kernel.route_blocks(t)
+    r = dict(
+        topk_idx=torch.empty((t, top_k), **i32), topk_w=torch.empty((t, top_k), **f32),
+        block_counts=torch.empty((nblk, e), **i32), block_base=torch.empty((nblk, e), **i32),
+        counts=torch.empty(e, **i32), offsets=torch.empty(e + 1, **i32),
+        mtile_offsets=torch.empty(e + 1, **i32), amax=torch.empty(1, **f32),
+        perm=torch.empty(rows, **i32), inv_perm=torch.empty(rows, **i32),
+        xp=torch.empty((rows, hidden), dtype=F8, device=dev),
+        xps=(torch.empty((hidden // GROUP, rows), **f32) if block else x_scale),
+        h=torch.empty((rows, inter), dtype=torch.bfloat16, device=dev),
+        hq=torch.empty((rows, inter), dtype=F8, device=dev),
+        hs=(torch.empty((inter // GROUP, rows), **f32) if block else torch.empty(1, **f32)),
+        y=torch.empty((rows, hidden), dtype=torch.bfloat16, device=dev),
+        out=torch.empty((t, hidden), dtype=torch.bfloat16, device=dev),
+    )
+    tk_kernel.dispatch_route_topk(logits, r["topk_idx"], r["topk_w"], r["block_counts"])
+    tk_kernel.dispatch_expert_offsets(r["block_counts"], t, r["counts"], r["offsets"],
+                                      r["block_base"], r["mtile_offsets"], r["amax"])
+    tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"],
+                               r["inv_perm"], x_q, x_scale if block else None, r["xp"],
+                               r["xps"] if block else None)
+    tk_kernel.dispatch_grouped_gemm1(r["xp"], r["xps"], w13_q, w13_scale, r["offsets"],
+                                     r["mtile_offsets"], r["h"], None if block else r["amax"])
+    tk_kernel.dispatch_requant(r["h"], None if block else r["amax"], r["hq"], r["hs"])
+    tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2_q, w2_scale, r["offsets"],
+                                     r["mtile_offsets"], r["y"])
+    tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])
+    return r
+
+
+class MoELayer:
+    """FP8 MoE FFN layer: e4m3 expert weights with per-tensor ([E]) or
+    128x128 block scales; runs hkmoe_moe_forward with a cached workspace."""
+
+    def __init__(self, w13_q, w13_scale, w2_q, w2_scale, top_k):
+        _check_dev(w13_q, w2_q)
+        if w13_q.dtype != F8 or w2_q.dtype != F8:
+            raise RuntimeError("MoELayer: weights must be float8_e4m3fn")
+        self.w13_q, self.w13_scale = w13_q.contiguous(), w13_scale.contiguous()
+        self.w2_q, self.w2_scale = w2_q.contiguous(), w2_scale.contiguous()
+        self.top_k = int(top_k)
+        self.num_experts, two_i, self.hidden = w13_q.shape
+        self.inter = two_i // 2
+        self.block = w13_scale.dim() == 3
+        self._ws = None
+
+    def workspace(self, num_tokens, device):
+        mode = tk_kernel.SCALE_BLOCK if self.block else tk_kernel.SCALE_TENSOR
+        need = tk_kernel.moe_workspace_size(num_tokens, self.num_experts, self.top_k, self.hidden,
+                                            self.inter, mode)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return self._ws
+
+    def __call__(self, x_q, x_scale, logits, out=None):
+        ws = self.workspace(x_q.shape[0], x_q.device)
+        return moe_forward(x_q, x_scale, logits, self.w13_q, self.w13_scale, self.w2_q,
+                           self.w2_scale, self.top_k, out=out, workspace=ws)

@@ -1,0 +1,180 @@
+/*
+ * hkmoe.h -- C ABI of the MI355X (gfx950) FP8 mixture-of-experts path.
+ *
+ * Plain pointers and sizes only (no torch types).  Every entry point:
+ *   - takes device pointers that the caller owns (outputs preallocated, as the
+ *     reference's dispatch functions expect: C is allocated by the caller in
+ *     kernels/cdna3/gemm/fp8fp32/mi300x/8192_256_256_64_32/data_logs/
+ *     0613_003858_outputs/test_python.py:12);
+ *   - enqueues asynchronously on `stream` (a hipStream_t; NULL = the null
+ *     stream) and never synchronises with the host; per-expert offsets stay on
+ *     the device;
+ *   - returns HKMOE_OK or an error code; hkmoe_last_error() then describes the
+ *     failure (thread-local).  Shape/size errors are detected on the host
+ *     before anything is launched, mirroring the std::runtime_error checks of
+ *     include/pyutils/pyutils.cuh:17-45.
+ *
+ * Formats: e4m3 = OCP float8 e4m3fn bytes; bf16 = bfloat16 bits; scales fp32.
+ * Tensor layouts are row-major; "[K/128, ld]" marks the transposed activation
+ * scale layout used inside the layer's workspace.
+ */
+#ifndef HKMOE_H
+#define HKMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* hkmoe_stream_t; /* hipStream_t */
+
+enum hkmoe_status {
+  HKMOE_OK = 0,
+  HKMOE_ERR_INVALID_ARGUMENT = 1,
+  HKMOE_ERR_UNSUPPORTED = 2,
+  HKMOE_ERR_HIP = 3,
+  HKMOE_ERR_WORKSPACE = 4
+};
+
+enum hkmoe_dtype { HKMOE_BF16 = 0, HKMOE_F32 = 1 };
+
+enum hkmoe_scale_mode {
+  HKMOE_SCALE_TENSOR = 0, /* one fp32 scale per tensor (weights: one per expert) */
+  HKMOE_SCALE_BLOCK = 1   /* activations 1x128 groups, weights 128x128 blocks */
+};
+
+/* Library version (major*10000 + minor*100 + patch) and last error text. */
+int hkmoe_version(void);
+const char* hkmoe_last_error(void);
+
+/*
+ * Dense FP8 GEMM  C[M,N] = (sa*sb) * sum_k A[m,k] * B[n,k]   (A . B^T, "TN")
+ *   A [M,K] e4m3, B [N,K] e4m3, C [M,N] bf16 (RNE) or fp32.
+ *   scale_a, scale_b: device fp32 scalars, or NULL for 1.0.
+ *   Requires K % 128 == 0 and N % 256 == 0; M is arbitrary.
+ * Replaces the reference's dispatch_micro(A, B, C) (C = A . B^T, fp32 out):
+ *   kernels/cdna3/gemm/fp8fp32/mi300x/8192_256_256_64_32/data_logs/
+ *   0613_003858_outputs/256_256_64_32.cpp:202-212 and the FP8 GEMM kernels named
+ *   by kernels/cdna4/gemm/fp8fp32/FP8_4wave/Makefile:5 (sources absent there).
+ */
+int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
+                   const float* scale_a, const float* scale_b, int out_dtype,
+                   hkmoe_stream_t stream);
+
+/*
+ * Routing step 1: top-k + softmax weights + per-block expert histogram.
+ *   logits [T,E] fp32 -> topk_idx [T,k] int32, topk_w [T,k] fp32.
+ *   Order: descending logit, ties to the lower expert id.  Weights: softmax
+ *   over the k selected logits.  block_counts: workspace [nblk, E] int32 with
+ *   nblk = hkmoe_route_blocks(T).  E <= 1024, 1 <= k <= min(E, 32).
+ * No reference counterpart (the reference has no router; SURVEY of
+ * /root/reference finds no top-k/softmax routing code).
+ */
+int hkmoe_route_blocks(int64_t num_tokens);
+int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                     int32_t* topk_idx, float* topk_w, int32_t* block_counts,
+                     hkmoe_stream_t stream);
+
+/*
+ * Routing step 2: expert offsets.  From block_counts [nblk, E] computes
+ *   counts [E], offsets [E+1] (exclusive prefix sum, offsets[E] = T*k),
+ *   block_base [nblk, E] (rows of expert e routed from earlier blocks),
+ *   mtile_offsets [E+1] (prefix sum of ceil(counts/256): the grouped GEMM's
+ *   M-tile list), and zeroes *amax_reset when non-NULL.
+ */
+int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
+                         int32_t* counts, int32_t* offsets, int32_t* block_base,
+                         int32_t* mtile_offsets, float* amax_reset, hkmoe_stream_t stream);
+
+/*
+ * Routing step 3: stable scatter into expert-contiguous order.
+ *   perm [T*k]: perm[p] = t*k + j (f ascending within an expert);
+ *   inv_perm [T*k]: inv_perm[t*k+j] = p.
+ *   When x_q is non-NULL also gathers rows: xp[p] = x_q[perm[p] / k] ([T*k, H]
+ *   e4m3) and, for HKMOE_SCALE_BLOCK, xp_scale_t[g, p] = x_scale[perm[p]/k, g]
+ *   (transposed [H/128, T*k]).
+ */
+int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                  const int32_t* offsets, const int32_t* block_base, int32_t* perm,
+                  int32_t* inv_perm, const void* x_q, const float* x_scale, int64_t hidden,
+                  int scale_mode, void* xp, float* xp_scale_t, hkmoe_stream_t stream);
+
+/*
+ * Grouped GEMM 1 with fused SiLU(gate)*up:
+ *   h[p, i] = bf16( silu(g) * u ),  [g | u] = deq(xp[p]) . deq(W13[e])^T
+ *   xp [R,H] e4m3 with R = T*k rows ordered by expert (offsets [E+1]);
+ *   w13 [E, 2I, H] e4m3 (gate rows 0..I-1, up rows I..2I-1);
+ *   TENSOR: xp_scale [1], w13_scale [E]; the max |h| is accumulated into
+ *           *amax (must be zeroed before; hkmoe_expert_offsets can do it).
+ *   BLOCK:  xp_scale_t [H/128, R], w13_scale [E, 2I/128, H/128].
+ *   Requires H % 128 == 0, I % 128 == 0.
+ */
+int hkmoe_grouped_gemm1(const void* xp, const float* xp_scale, const void* w13,
+                        const float* w13_scale, const int32_t* offsets,
+                        const int32_t* mtile_offsets, int64_t rows, int32_t num_experts,
+                        int32_t hidden, int32_t inter, int scale_mode, void* h, float* amax,
+                        hkmoe_stream_t stream);
+
+/*
+ * Requantise the bf16 intermediate to e4m3 for GEMM 2.
+ *   TENSOR: hs[0] = scale(amax), hq = e4m3(h / hs[0]) (amax from GEMM 1).
+ *   BLOCK:  1x128 groups, hs_t [I/128, R] (transposed) = amax_g / 448.
+ */
+int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, const float* amax,
+                  void* hq, float* hs, hkmoe_stream_t stream);
+
+/*
+ * Grouped GEMM 2:  y[p] = bf16( deq(hq[p]) . deq(W2[e])^T ),  w2 [E, H, I].
+ *   TENSOR: hs [1], w2_scale [E];  BLOCK: hs_t [I/128, R], w2_scale [E, H/128, I/128].
+ *   Requires H % 256 == 0, I % 128 == 0.
+ */
+int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
+                        const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
+                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
+                        void* y, hkmoe_stream_t stream);
+
+/*
+ * Top-k weighted unpermute/combine:
+ *   out[t] = bf16( sum_{j<k} topk_w[t,j] * y[inv_perm[t*k+j]] ), fp32 accumulate.
+ *   y [T*k, H] bf16, out [T, H] bf16, H % 8 == 0.
+ */
+int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, int64_t num_tokens,
+                  int32_t top_k, int32_t hidden, void* out, hkmoe_stream_t stream);
+
+/*
+ * Whole layer: route -> scatter -> GEMM1+SiLU*up -> requant -> GEMM2 -> combine.
+ *   x_q [T,H] e4m3; x_scale [1] (TENSOR) or [T, H/128] (BLOCK);
+ *   logits [T,E] fp32; w13/w2 and scales as above; out [T,H] bf16.
+ *   workspace: device buffer of hkmoe_moe_workspace_size(...) bytes, 256-byte
+ *   aligned.  Optional outputs (may be NULL): topk_idx [T,k] int32,
+ *   topk_w [T,k] fp32 are written into the workspace otherwise.
+ */
+size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k,
+                                int32_t hidden, int32_t inter, int scale_mode);
+int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
+                      const float* w13_scale, const void* w2, const float* w2_scale,
+                      int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
+                      int32_t inter, int scale_mode, void* out, void* workspace,
+                      size_t workspace_bytes, hkmoe_stream_t stream);
+
+/*
+ * Synthetic-input helpers (quantisers): x [R, C] fp32 on the device.
+ *   hkmoe_quant_group:  q [R,C] e4m3, s [R, C/128]  (1x128 groups, row-major s)
+ *   hkmoe_quant_block:  q [B,R,C] e4m3, s [B, R/128, C/128] (128x128 blocks)
+ *   hkmoe_quant_tensor: q [R,C], s [1]; amax_ws: one fp32 of device scratch.
+ * Scale = amax/448 (1.0 for an all-zero block); q = e4m3(x / s) RNE, saturating.
+ */
+int hkmoe_quant_group(const float* x, int64_t rows, int64_t cols, void* q, float* s,
+                      hkmoe_stream_t stream);
+int hkmoe_quant_block(const float* x, int64_t batch, int64_t rows, int64_t cols, void* q, float* s,
+                      hkmoe_stream_t stream);
+int hkmoe_quant_tensor(const float* x, int64_t rows, int64_t cols, void* q, float* s,
+                       float* amax_ws, hkmoe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HKMOE_H */

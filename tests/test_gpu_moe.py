@@ -1,0 +1,182 @@
+"""MoE path through the native kernels vs the oracle (same seeded inputs).
+
+Bars (from the path's specification):
+  * bit-exact: top-k indices, counts, offsets, M-tile offsets, perm, inv_perm,
+    the gathered expert-contiguous rows and scales, requantised bytes/scales
+    (fed the GPU's own bf16 intermediate), device quantisers;
+  * routing weights: max relative error <= 1e-6 (fp32 exp/divide);
+  * GEMM and combine outputs: max|got - ref| / max|ref| <= 1e-2, ref = the
+    fp32 value before the bf16 store.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_np, f8_np, moe_inputs_to_gpu, rel_err, to_f32
+from oracle import spec, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+SMALL = {
+    "tensor_e8k2": dict(T=96, H=512, I=256, E=8, k=2, block=False, skew=False),
+    "block_e16k4_skew": dict(T=130, H=512, I=256, E=16, k=4, block=True, skew=True),
+    "block_e64k8_skew": dict(T=300, H=768, I=384, E=64, k=8, block=True, skew=True),
+    "tensor_e5k5": dict(T=33, H=256, I=128, E=5, k=5, block=False, skew=False),
+    "block_t1": dict(T=1, H=256, I=128, E=4, k=2, block=True, skew=False),
+}
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _run_steps(hk, g):
+    r = hk.moe_forward_steps(g["x_q"], g["x_scale"], g["logits"], g["w13_q"], g["w13_scale"],
+                             g["w2_q"], g["w2_scale"], g["top_k"])
+    torch.cuda.synchronize()
+    return r
+
+
+@pytest.mark.parametrize("name", list(SMALL))
+def test_moe_stepwise_parity(hk, name):
+    d = synth.make_moe(seed=11, **SMALL[name])
+    g = moe_inputs_to_gpu(d)
+    r = _run_steps(hk, g)
+    ref = spec.moe_forward(d["x_q"], d["x_scale"], d["logits"], d["w13_q"], d["w13_s"], d["w2_q"],
+                           d["w2_s"], d["k"], return_all=True)
+    block = SMALL[name]["block"]
+    k = d["k"]
+    # routing: bit-exact
+    np.testing.assert_array_equal(_np(r["topk_idx"]), ref["topk_idx"])
+    assert rel_err(_np(r["topk_w"]), ref["topk_w"]) <= 1e-6
+    np.testing.assert_array_equal(_np(r["counts"]), ref["counts"])
+    np.testing.assert_array_equal(_np(r["offsets"]), ref["offsets"])
+    mt = np.concatenate([[0], np.cumsum((ref["counts"] + 255) // 256)])
+    np.testing.assert_array_equal(_np(r["mtile_offsets"]), mt)
+    np.testing.assert_array_equal(_np(r["perm"]), ref["perm"])
+    np.testing.assert_array_equal(_np(r["inv_perm"]), ref["inv_perm"])
+    np.testing.assert_array_equal(f8_np(r["xp"]), ref["xp"])
+    if block:
+        np.testing.assert_array_equal(_np(r["xps"]).T, ref["xps"])
+    # GEMM1 + SiLU*up, fed identical inputs: tolerance vs fp32
+    h = bf16_np(r["h"])
+    h_ref32 = spec.gemm1_silu(ref["xp"], ref["xps"], d["w13_q"], d["w13_s"], ref["offsets"], rounded=False)
+    assert rel_err(h, h_ref32) <= TOL
+    # requant of the GPU's own h: bit-exact
+    hq_ref, hs_ref = spec.requant(h, block)
+    np.testing.assert_array_equal(f8_np(r["hq"]), hq_ref)
+    if block:
+        np.testing.assert_array_equal(_np(r["hs"]).T, hs_ref)
+    else:
+        assert _np(r["hs"])[0] == hs_ref
+    # GEMM2 from the GPU's own hq
+    y_ref32 = spec.gemm2(hq_ref, hs_ref, d["w2_q"], d["w2_s"], ref["offsets"], rounded=False)
+    assert rel_err(bf16_np(r["y"]), y_ref32) <= TOL
+    # combine from the GPU's own y
+    out_ref32 = spec.combine(bf16_np(r["y"]), _np(r["topk_w"]), ref["inv_perm"], rounded=False)
+    assert rel_err(bf16_np(r["out"]), out_ref32) <= TOL
+    # end to end against the oracle's own pipeline
+    assert rel_err(bf16_np(r["out"]), ref["out_f32"]) <= TOL
+    del k
+
+
+@pytest.mark.parametrize("name", ["tensor_e8k2", "block_e16k4_skew"])
+def test_moe_single_call_matches_steps(hk, name):
+    """hkmoe_moe_forward (one C call, carved workspace) == the stepwise path, bit for bit."""
+    d = synth.make_moe(seed=12, **SMALL[name])
+    g = moe_inputs_to_gpu(d)
+    r = _run_steps(hk, g)
+    out = hk.moe_forward(g["x_q"], g["x_scale"], g["logits"], g["w13_q"], g["w13_scale"],
+                         g["w2_q"], g["w2_scale"], g["top_k"])
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), r["out"].view(torch.int16))
+    # second call with a reused (dirty) workspace gives the same bits
+    layer = hk.MoELayer(g["w13_q"], g["w13_scale"], g["w2_q"], g["w2_scale"], g["top_k"])
+    o1 = layer(g["x_q"], g["x_scale"], g["logits"]).clone()
+    o2 = layer(g["x_q"], g["x_scale"], g["logits"])
+    torch.cuda.synchronize()
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(o1.view(torch.int16), out.view(torch.int16))
+
+
+def test_routing_ties_and_edges(hk):
+    """Ties resolve to the lower expert id; T not a multiple of the block; E not a power of 2."""
+    rng = np.random.default_rng(3)
+    for t, e, k in [(1, 1, 1), (45, 100, 7), (70, 256, 8), (33, 1024, 32), (64, 3, 3)]:
+        logits = np.round(rng.standard_normal((t, e)).astype(np.float32) * 2) / 2  # many ties
+        idx_ref, w_ref = spec.route_topk(logits, k)
+        lg = to_f32(logits)
+        nblk = hk.tk_kernel.route_blocks(t)
+        idx = torch.empty((t, k), dtype=torch.int32, device="cuda")
+        w = torch.empty((t, k), dtype=torch.float32, device="cuda")
+        bc = torch.empty((nblk, e), dtype=torch.int32, device="cuda")
+        hk.tk_kernel.dispatch_route_topk(lg, idx, w, bc)
+        counts = torch.empty(e, dtype=torch.int32, device="cuda")
+        offs = torch.empty(e + 1, dtype=torch.int32, device="cuda")
+        bb = torch.empty_like(bc)
+        mto = torch.empty(e + 1, dtype=torch.int32, device="cuda")
+        hk.tk_kernel.dispatch_expert_offsets(bc, t, counts, offs, bb, mto, None)
+        perm = torch.empty(t * k, dtype=torch.int32, device="cuda")
+        inv = torch.empty(t * k, dtype=torch.int32, device="cuda")
+        hk.tk_kernel.dispatch_scatter(idx, offs, bb, perm, inv, None, None, None, None)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(idx), idx_ref)
+        assert rel_err(_np(w), w_ref) <= 1e-6
+        c_ref, o_ref = spec.expert_counts_offsets(idx_ref, e)
+        np.testing.assert_array_equal(_np(counts), c_ref)
+        np.testing.assert_array_equal(_np(offs), o_ref)
+        p_ref, i_ref = spec.permutation(idx_ref, e)
+        np.testing.assert_array_equal(_np(perm), p_ref)
+        np.testing.assert_array_equal(_np(inv), i_ref)
+
+
+@pytest.mark.parametrize("name", ["dsv3", "mixtral", "decode"])
+def test_routing_full_size(hk, name):
+    """Routing + offsets + permutation at the full configurations' T, E, k: bit-exact."""
+    cfg = synth.CONFIGS[name]
+    rng = np.random.default_rng(0)
+    rng.standard_normal((1, 1))  # independent stream; shapes are what matters here
+    logits = synth.make_logits(rng, cfg["T"], cfg["E"], cfg["skew"])
+    t, e, k = cfg["T"], cfg["E"], cfg["k"]
+    idx_ref, w_ref = spec.route_topk(logits, k)
+    nblk = hk.tk_kernel.route_blocks(t)
+    idx = torch.empty((t, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((t, k), dtype=torch.float32, device="cuda")
+    bc = torch.empty((nblk, e), dtype=torch.int32, device="cuda")
+    hk.tk_kernel.dispatch_route_topk(to_f32(logits), idx, w, bc)
+    counts = torch.empty(e, dtype=torch.int32, device="cuda")
+    offs = torch.empty(e + 1, dtype=torch.int32, device="cuda")
+    bb = torch.empty_like(bc)
+    mto = torch.empty(e + 1, dtype=torch.int32, device="cuda")
+    hk.tk_kernel.dispatch_expert_offsets(bc, t, counts, offs, bb, mto, None)
+    perm = torch.empty(t * k, dtype=torch.int32, device="cuda")
+    inv = torch.empty(t * k, dtype=torch.int32, device="cuda")
+    hk.tk_kernel.dispatch_scatter(idx, offs, bb, perm, inv, None, None, None, None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_np(idx), idx_ref)
+    assert rel_err(_np(w), w_ref) <= 1e-6
+    p_ref, i_ref = spec.permutation(idx_ref, e)
+    np.testing.assert_array_equal(_np(perm), p_ref)
+    np.testing.assert_array_equal(_np(inv), i_ref)
+    assert _np(offs)[-1] == t * k
+
+
+def test_quantisers_bit_exact(hk):
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((256, 384)) * 3).astype(np.float32)
+    x[5, :128] = 0.0  # an all-zero group -> scale 1.0
+    q, s = hk.quant_group(to_f32(x))
+    q_ref, s_ref = spec.quant_group_1x128(x)
+    np.testing.assert_array_equal(f8_np(q), q_ref)
+    np.testing.assert_array_equal(_np(s), s_ref)
+    w = rng.standard_normal((3, 256, 384)).astype(np.float32)
+    q, s = hk.quant_block(to_f32(w))
+    q_ref, s_ref = spec.quant_block_128x128(w)
+    np.testing.assert_array_equal(f8_np(q), q_ref)
+    np.testing.assert_array_equal(_np(s), s_ref)
+    q, s = hk.quant_tensor(to_f32(x))
+    q_ref, s_ref = spec.quant_per_tensor(x)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(f8_np(q), q_ref)
+    assert _np(s)[0] == s_ref
