@@ -1,0 +1,253 @@
+"""Benchmark: FP8 MoE grouped-GEMM TFLOP/s and % of dense-FP8 MFMA peak on 1 MI355X.
+
+One step = one full MoE layer forward through the native path
+(route -> scatter -> grouped GEMM1 + SiLU*up -> requant -> grouped GEMM2 ->
+combine) on inputs already resident in HBM.  ``value`` = the layer's GEMM
+FLOPs (2*rows*2I*H + 2*rows*H*I, rows = T*k) / measured step time, i.e. the
+routing, permute, requant and combine kernels count against the number.
+
+Default workload: the DeepSeek-V3-shape layer (T=8192, H=7168, I=2048, E=256,
+top-8, Zipf-skewed routing, 128x128 weight / 1x128 activation block scales).
+Synthetic inputs are drawn on the GPU (torch generator, N(0,1)) and quantised
+by the path's own device quantisers.
+
+Extra JSON fields: ``roofline`` (dominant kernel: grouped GEMM 1, timed with
+events on the stream it runs on), ``cpu_baseline`` (the oracle's dequantise +
+fp32 per-expert matmul path on a bounded sample of experts, host cores),
+``kernels`` (per-kernel average ms from an event-timed stepwise pass).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "distributed-hipkittens_amd"))
+
+METRIC = "fp8 MoE grouped-GEMM TFLOP/s + % of FP8 MFMA peak on 1 MI355X"
+PEAK_FP8_TFLOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    "dsv3": dict(T=8192, H=7168, I=2048, E=256, k=8, block=True, skew=True),
+    "mixtral": dict(T=4096, H=4096, I=14336, E=8, k=2, block=False, skew=False),
+    "decode": dict(T=64, H=4096, I=1536, E=128, k=8, block=True, skew=False),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="dsv3", choices=sorted(CONFIGS))
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="time budget of the bounded CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
+                    help="measured HBM bytes per launch (rocprofv3 --pmc summary)")
+    return ap.parse_args()
+
+
+def make_inputs(cfg, seed, dev):
+    import torch
+    import hkmoe
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    T, H, I, E, k = cfg["T"], cfg["H"], cfg["I"], cfg["E"], cfg["k"]
+    x = torch.randn((T, H), generator=g, device=dev, dtype=torch.float32)
+    logits = torch.randn((T, E), generator=g, device=dev, dtype=torch.float32)
+    if cfg["skew"]:
+        rank = torch.randperm(E, generator=g, device=dev).float() + 1.0
+        logits += (-1.1 * torch.log(rank))[None, :]
+    F8 = torch.float8_e4m3fn
+    w13_q = torch.empty((E, 2 * I, H), dtype=F8, device=dev)
+    w2_q = torch.empty((E, H, I), dtype=F8, device=dev)
+    if cfg["block"]:
+        x_q, x_s = hkmoe.quant_group(x)
+        w13_s = torch.empty((E, 2 * I // 128, H // 128), dtype=torch.float32, device=dev)
+        w2_s = torch.empty((E, H // 128, I // 128), dtype=torch.float32, device=dev)
+    else:
+        x_q, x_s = hkmoe.quant_tensor(x)
+        w13_s = torch.empty(E, dtype=torch.float32, device=dev)
+        w2_s = torch.empty(E, dtype=torch.float32, device=dev)
+    del x
+    chunk = max(1, int(2e9 // (2 * I * H * 4)))
+    for e0 in range(0, E, chunk):
+        e1 = min(E, e0 + chunk)
+        for wq, ws, shape in ((w13_q, w13_s, (2 * I, H)), (w2_q, w2_s, (H, I))):
+            w = torch.randn((e1 - e0, *shape), generator=g, device=dev, dtype=torch.float32)
+            if cfg["block"]:
+                q, s = hkmoe.quant_block(w)
+                wq[e0:e1].copy_(q)
+                ws[e0:e1].copy_(s)
+            else:
+                for e in range(e0, e1):
+                    q, s = hkmoe.quant_tensor(w[e - e0])
+                    wq[e].copy_(q)
+                    ws[e:e + 1].copy_(s)
+            del w
+    torch.cuda.synchronize()
+    return dict(x_q=x_q, x_scale=x_s, logits=logits, w13_q=w13_q, w13_scale=w13_s, w2_q=w2_q,
+                w2_scale=w2_s, top_k=k)
+
+
+def gemm_flops(cfg):
+    rows = cfg["T"] * cfg["k"]
+    return 2.0 * rows * (2 * cfg["I"]) * cfg["H"] + 2.0 * rows * cfg["H"] * cfg["I"]
+
+
+def kernel_breakdown(inp, iters=10):
+    """Average ms of each kernel of the stepwise layer, events on torch's current
+    stream (the stream every dispatch_* call launches on)."""
+    import torch
+    import tk_kernel
+    import hkmoe
+    r = hkmoe.moe_forward_steps(inp["x_q"], inp["x_scale"], inp["logits"], inp["w13_q"],
+                                inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"])
+    block = inp["x_scale"].dim() == 2
+    T = inp["x_q"].shape[0]
+    k = inp["top_k"]
+    calls = [
+        ("route_topk", lambda: tk_kernel.dispatch_route_topk(inp["logits"], r["topk_idx"], r["topk_w"], r["block_counts"])),
+        ("expert_offsets", lambda: tk_kernel.dispatch_expert_offsets(r["block_counts"], T, r["counts"], r["offsets"], r["block_base"], r["mtile_offsets"], r["amax"])),
+        ("scatter", lambda: tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"], r["inv_perm"], None, None, None, None)),
+    ]
+    if block:
+        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, inp["w13_q"], inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"])))
+    else:
+        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, inp["w13_q"], inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["h"], r["amax"])))
+        calls.append(("requant", lambda: tk_kernel.dispatch_requant(r["h"], r["amax"], r["hq"], r["hs"])))
+    calls += [
+        ("grouped_gemm2", lambda: tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], inp["w2_q"], inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"])),
+        ("combine", lambda: tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])),
+    ]
+    ev = {name: [] for name, _ in calls}
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        for name, fn in calls:
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            ev[name].append((s, e))
+    torch.cuda.synchronize()
+    ms = {name: sum(s.elapsed_time(e) for s, e in lst) / len(lst) for name, lst in ev.items()}
+    return ms, r
+
+
+def cpu_baseline(inp, cfg, budget_s):
+    """Oracle (numpy) dequantise + fp32 per-expert GEMMs on a bounded sample of
+    experts (descending load), timed on the host; TFLOP/s of the sampled work."""
+    import numpy as np
+    from oracle import spec
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    logits = inp["logits"].cpu().numpy()
+    idx, _ = spec.route_topk(logits, cfg["k"])
+    counts, offsets = spec.expert_counts_offsets(idx, cfg["E"])
+    perm, _ = spec.permutation(idx, cfg["E"])
+    x_q = inp["x_q"].view(__import__("torch").uint8).cpu().numpy()
+    xs = inp["x_scale"].cpu().numpy()
+    block = cfg["block"]
+    xs = xs if block else np.float32(xs.reshape(-1)[0])
+    order = np.argsort(-counts, kind="stable")
+    flops = 0.0
+    experts = []
+    t_start = time.perf_counter()
+    elapsed = 0.0
+    for e in order:
+        if counts[e] == 0 or elapsed > budget_s:
+            break
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        tok = perm[lo:hi] // cfg["k"]
+        w13 = inp["w13_q"][e].view(__import__("torch").uint8).cpu().numpy()
+        w2 = inp["w2_q"][e].view(__import__("torch").uint8).cpu().numpy()
+        s13 = inp["w13_scale"][e].cpu().numpy()
+        s2 = inp["w2_scale"][e].cpu().numpy()
+        t0 = time.perf_counter()
+        xa = spec.dequant_act(x_q[tok], xs[tok] if block else xs)
+        z = xa @ spec.dequant_weight(w13, s13).T
+        h = spec.bf16_round(spec.silu_mul(z[:, :cfg["I"]], z[:, cfg["I"]:]))
+        hq, hs = spec.requant(h, block)
+        _ = spec.bf16_round(spec.dequant_act(hq, hs) @ spec.dequant_weight(w2, s2).T)
+        elapsed += time.perf_counter() - t0
+        flops += 2.0 * (hi - lo) * 3 * cfg["I"] * cfg["H"]
+        experts.append(int(e))
+    del t_start
+    return {"value": flops / elapsed / 1e12 if elapsed > 0 else None, "unit": "TFLOP/s",
+            "cores": int(threads), "kind": "port",
+            "sample": f"{len(experts)} of {int((counts > 0).sum())} active experts (heaviest first, "
+                      f"{int(sum(counts[e] for e in experts))} rows), numpy fp32 dequantise + matmul, "
+                      f"{elapsed:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: run with --gpus 1 "
+                                   "(multi-GPU sharding is a design note, not a measured path)"}))
+        sys.exit(2)
+    import torch
+    import hkmoe
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = CONFIGS[args.config]
+    inp = make_inputs(cfg, args.seed, dev)
+    layer = hkmoe.MoELayer(inp["w13_q"], inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"])
+    out = torch.empty((cfg["T"], cfg["H"]), dtype=torch.bfloat16, device=dev)
+    for _ in range(args.warmup):
+        layer(inp["x_q"], inp["x_scale"], inp["logits"], out=out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        layer(inp["x_q"], inp["x_scale"], inp["logits"], out=out)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    flops = gemm_flops(cfg)
+    value = flops / dt / 1e12
+
+    ms, r = kernel_breakdown(inp)
+    rows = cfg["T"] * cfg["k"]
+    g1_flops = 2.0 * rows * 2 * cfg["I"] * cfg["H"]
+    g1_tflops = g1_flops / (ms["grouped_gemm1"] * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(args.traffic):
+        try:
+            with open(args.traffic) as f:
+                traffic = json.load(f).get(f"{args.config}:grouped_gemm1")
+        except Exception:
+            traffic = None
+    counts = r["counts"].cpu()
+    res = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "e4m3",
+        "data": "synthetic (seeded torch N(0,1) on device, quantised by the path's quantisers)",
+        "config": {"workload": f"{args.config}_moe_layer", "T": cfg["T"], "hidden": cfg["H"],
+                   "inter": cfg["I"], "experts": cfg["E"], "top_k": cfg["k"],
+                   "scales": "128x128 weight / 1x128 activation blocks" if cfg["block"] else "per-tensor",
+                   "routing": "zipf(1.1) skew" if cfg["skew"] else "N(0,1) logits",
+                   "active_experts": int((counts > 0).sum()), "max_rows": int(counts.max())},
+        "pct_fp8_peak": round(100.0 * value / PEAK_FP8_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "kernel": "grouped_gemm1 (gate/up + SiLU*up)",
+                     "achieved": round(g1_tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(g1_tflops / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
+                     "avg_ms": round(ms["grouped_gemm1"], 4), "flops_per_launch": g1_flops},
+        "kernels_ms": {k: round(v, 4) for k, v in ms.items()},
+        "gemm_only_tflops": round(flops / ((ms["grouped_gemm1"] + ms["grouped_gemm2"]) * 1e-3) / 1e12, 2),
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(inp, cfg, args.cpu_seconds)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -119,6 +119,7 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
   p.a_scale = scale_a;
   p.b_scale = scale_b;
   p.rows = m;
+  p.a_rows = m;
   p.num_experts = 1;
   p.K = static_cast<int32_t>(k);
   p.nb = static_cast<int32_t>(n);
@@ -194,39 +195,58 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
   return check_launch("scatter_kernel");
 }
 
-int hkmoe_grouped_gemm1(const void* xp, const float* xp_scale, const void* w13,
-                        const float* w13_scale, const int32_t* offsets, const int32_t* mtile_offsets,
-                        int64_t rows, int32_t num_experts, int32_t hidden, int32_t inter,
-                        int scale_mode, void* h, float* amax, hkmoe_stream_t stream) {
-  HK_REQUIRE(xp && w13 && offsets && mtile_offsets && h, "grouped_gemm1: null pointer");
-  HK_REQUIRE(xp_scale && w13_scale, "grouped_gemm1: null scale pointer");
+int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gather,
+                        int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
+                        const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
+                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
+                        int out_format, void* h, float* h_aux, hkmoe_stream_t stream) {
+  HK_REQUIRE(x && w13 && offsets && mtile_offsets && h, "grouped_gemm1: null pointer");
+  HK_REQUIRE(x_scale && w13_scale, "grouped_gemm1: null scale pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1: bad E=%d", num_experts);
-  HK_REQUIRE(hidden > 0 && hidden % kBK == 0, "grouped_gemm1: hidden=%d must be a multiple of 128", hidden);
+  HK_REQUIRE(hidden > 0 && hidden % kBK == 0 && hidden <= kBK * kMaxKBlocks,
+             "grouped_gemm1: hidden=%d must be a multiple of 128 and <= %d", hidden, kBK * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "grouped_gemm1: inter=%d must be a multiple of 128", inter);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm1: bad rows");
+  HK_REQUIRE(x_rows >= 1 && x_rows * hidden < (1ll << 32), "grouped_gemm1: x_rows=%lld out of range",
+             (long long)x_rows);
+  HK_REQUIRE(gather == nullptr || gather_div >= 1, "grouped_gemm1: gather_div must be >= 1");
+  HK_REQUIRE(gather != nullptr || x_rows >= rows, "grouped_gemm1: x has fewer rows than rows");
   HK_REQUIRE(2ll * inter * hidden < (1ll << 32), "grouped_gemm1: expert weight too large");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
              "grouped_gemm1: bad scale_mode %d", scale_mode);
+  HK_REQUIRE(out_format == HKMOE_BF16 || (out_format == HKMOE_E4M3 && scale_mode == HKMOE_SCALE_BLOCK),
+             "grouped_gemm1: out_format %d not supported with scale_mode %d", out_format, scale_mode);
+  HK_REQUIRE(out_format != HKMOE_E4M3 || h_aux != nullptr, "grouped_gemm1: e4m3 output needs h_aux scales");
   if (rows == 0) return HKMOE_OK;
   GemmParams p{};
-  p.a = static_cast<const uint8_t*>(xp);
+  p.a = static_cast<const uint8_t*>(x);
+  p.a_gather = gather;
+  p.gather_div = gather ? gather_div : 1;
   p.b = static_cast<const uint8_t*>(w13);
   p.c = h;
-  p.a_scale = xp_scale;
+  p.a_scale = x_scale;
   p.b_scale = w13_scale;
   p.offsets = offsets;
   p.mtile_offsets = mtile_offsets;
-  p.amax = amax;
   p.rows = rows;
-  p.a_scale_ld = rows;
+  p.a_rows = x_rows;
+  p.as_rs = hidden / kGroup;  // x_scale is row-major [x_rows, H/128]
+  p.as_ks = 1;
   p.num_experts = num_experts;
   p.K = hidden;
   p.nb = 2 * inter;
   p.n_out = inter;
   p.n_tiles = inter / 128;
   auto s = static_cast<hipStream_t>(stream);
-  return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kSiluBf16, Scale::kBlock>(p, s)
-                                         : launch_gemm<Epi::kSiluBf16, Scale::kTensor>(p, s);
+  if (scale_mode == HKMOE_SCALE_TENSOR) {
+    p.amax = h_aux;
+    return launch_gemm<Epi::kSiluBf16, Scale::kTensor>(p, s);
+  }
+  if (out_format == HKMOE_E4M3) {
+    p.c_scale = h_aux;
+    return launch_gemm<Epi::kSiluQuant, Scale::kBlock>(p, s);
+  }
+  return launch_gemm<Epi::kSiluBf16, Scale::kBlock>(p, s);
 }
 
 int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, const float* amax,
@@ -258,7 +278,8 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
   HK_REQUIRE(hq && hs && w2 && w2_scale && offsets && mtile_offsets && y, "grouped_gemm2: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2: hidden=%d must be a multiple of 256", hidden);
-  HK_REQUIRE(inter > 0 && inter % kBK == 0, "grouped_gemm2: inter=%d must be a multiple of 128", inter);
+  HK_REQUIRE(inter > 0 && inter % kBK == 0 && inter <= kBK * kMaxKBlocks,
+             "grouped_gemm2: inter=%d must be a multiple of 128 and <= %d", inter, kBK * kMaxKBlocks);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm2: bad rows");
   HK_REQUIRE(static_cast<int64_t>(hidden) * inter < (1ll << 32), "grouped_gemm2: expert weight too large");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
@@ -273,7 +294,9 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
   p.offsets = offsets;
   p.mtile_offsets = mtile_offsets;
   p.rows = rows;
-  p.a_scale_ld = rows;
+  p.a_rows = rows;
+  p.as_rs = 1;  // group scales are transposed [I/128, rows]
+  p.as_ks = rows;
   p.num_experts = num_experts;
   p.K = inter;
   p.nb = hidden;
@@ -312,9 +335,7 @@ struct MoeWorkspace {
   float* amax;
   int32_t* perm;
   int32_t* inv_perm;
-  uint8_t* xp;
-  float* xps_t;
-  uint16_t* h;
+  uint16_t* h;   // per-tensor mode only: bf16 intermediate before requantisation
   uint8_t* hq;
   float* hs;
   uint16_t* y;
@@ -342,9 +363,7 @@ MoeWorkspace carve(uint8_t* base, int64_t t, int32_t e, int32_t k, int32_t hidde
   w.amax = reinterpret_cast<float*>(take(4));
   w.perm = reinterpret_cast<int32_t*>(take(r * 4));
   w.inv_perm = reinterpret_cast<int32_t*>(take(r * 4));
-  w.xp = take(r * hidden);
-  w.xps_t = reinterpret_cast<float*>(take(block ? r * (hidden / kGroup) * 4 : 4));
-  w.h = reinterpret_cast<uint16_t*>(take(r * inter * 2));
+  w.h = block ? nullptr : reinterpret_cast<uint16_t*>(take(r * inter * 2));
   w.hq = take(r * inter);
   w.hs = reinterpret_cast<float*>(take(block ? r * (inter / kGroup) * 4 : 4));
   w.y = reinterpret_cast<uint16_t*>(take(r * hidden * 2));
@@ -373,7 +392,8 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "moe_forward: E=%d outside [1, %d]",
              num_experts, kMaxExperts);
   HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK, "moe_forward: bad top_k=%d", top_k);
-  HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "moe_forward: hidden=%d must be a multiple of 256", hidden);
+  HK_REQUIRE(hidden > 0 && hidden % kBN == 0 && hidden <= kBK * kMaxKBlocks,
+             "moe_forward: hidden=%d must be a multiple of 256 and <= %d", hidden, kBK * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "moe_forward: inter=%d must be a multiple of 128", inter);
   const bool block = scale_mode == HKMOE_SCALE_BLOCK;
   const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, block);
@@ -390,11 +410,19 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
   HK_TRY(hkmoe_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets,
                               w.block_base, w.mtile_offsets, w.amax, stream));
   HK_TRY(hkmoe_scatter(w.topk_idx, num_tokens, num_experts, top_k, w.offsets, w.block_base, w.perm,
-                       w.inv_perm, x_q, x_scale, hidden, scale_mode, w.xp, w.xps_t, stream));
-  HK_TRY(hkmoe_grouped_gemm1(w.xp, block ? w.xps_t : x_scale, w13, w13_scale, w.offsets,
-                             w.mtile_offsets, rows, num_experts, hidden, inter, scale_mode, w.h,
-                             w.amax, stream));
-  HK_TRY(hkmoe_requant(w.h, rows, inter, scale_mode, w.amax, w.hq, w.hs, stream));
+                       w.inv_perm, nullptr, nullptr, hidden, scale_mode, nullptr, nullptr, stream));
+  if (block) {
+    // GEMM 1 reads token rows through perm and writes the requantised e4m3
+    // intermediate and its 1x128 group scales directly.
+    HK_TRY(hkmoe_grouped_gemm1(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
+                               w.mtile_offsets, rows, num_experts, hidden, inter, scale_mode,
+                               HKMOE_E4M3, w.hq, w.hs, stream));
+  } else {
+    HK_TRY(hkmoe_grouped_gemm1(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
+                               w.mtile_offsets, rows, num_experts, hidden, inter, scale_mode,
+                               HKMOE_BF16, w.h, w.amax, stream));
+    HK_TRY(hkmoe_requant(w.h, rows, inter, scale_mode, w.amax, w.hq, w.hs, stream));
+  }
   HK_TRY(hkmoe_grouped_gemm2(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, rows, num_experts,
                              hidden, inter, scale_mode, w.y, stream));
   HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));

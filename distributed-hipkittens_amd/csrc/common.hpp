@@ -53,6 +53,13 @@ __device__ __forceinline__ void load_lds_16B(i32x4 rsrc, void* lds_base, int vof
                          16, voffset, 0, 0, 0);
 }
 
+// Same with 4 bytes per lane (lane i -> lds_base + 4*i).
+__device__ __forceinline__ void load_lds_4B(i32x4 rsrc, void* lds_base, int voffset) {
+  hk_raw_buffer_load_lds(rsrc, reinterpret_cast<HK_LDS uint32_t*>(
+                                   reinterpret_cast<uintptr_t>(lds_base)),
+                         4, voffset, 0, 0, 0);
+}
+
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------------------
@@ -117,8 +124,11 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t q) {
   return __uint_as_float(__float_as_uint(v) | s);
 }
 
+// Scale of a quantisation group: amax / 448, floored at the smallest normal
+// fp32 (2^-126) so every scale is a positive normal number; 1 for an all-zero
+// group.
 __device__ __forceinline__ float scale_from_amax(float amax) {
-  return amax > 0.0f ? amax / 448.0f : 1.0f;
+  return amax > 0.0f ? fmaxf(amax / 448.0f, 1.17549435e-38f) : 1.0f;
 }
 
 // ---------------------------------------------------------------------------

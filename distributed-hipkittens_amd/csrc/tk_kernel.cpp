@@ -193,34 +193,44 @@ void dispatch_scatter(py::object idx, py::object offsets, py::object block_base,
                       mode, d.ptr, static_cast<float*>(ds.ptr), current_stream()));
 }
 
-void dispatch_grouped_gemm1(py::object xp, py::object xps, py::object w13, py::object w13s,
-                            py::object offsets, py::object mtile_offsets, py::object h, py::object amax) {
-  auto x = as_tensor(xp, "xp"), xs = as_tensor(xps, "xp_scale"), w = as_tensor(w13, "w13"),
-       ws = as_tensor(w13s, "w13_scale"), o = as_tensor(offsets, "offsets"),
+void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gather, int32_t gather_div,
+                            py::object w13, py::object w13s, py::object offsets, py::object mtile_offsets,
+                            py::object h, py::object h_aux) {
+  auto x = as_tensor(x_q, "x"), xs = as_tensor(x_scale, "x_scale"), gth = as_tensor_opt(gather, "gather"),
+       w = as_tensor(w13, "w13"), ws = as_tensor(w13s, "w13_scale"), o = as_tensor(offsets, "offsets"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), hh = as_tensor(h, "h"),
-       am = as_tensor_opt(amax, "amax");
-  want_dtype(x, "xp", kF8);
+       aux = as_tensor_opt(h_aux, "h_aux");
+  want_dtype(x, "x", kF8);
   want_dtype(w, "w13", kF8);
-  want_dtype(xs, "xp_scale", kF32);
+  want_dtype(xs, "x_scale", kF32);
   want_dtype(ws, "w13_scale", kF32);
-  want_dtype(hh, "h", kBf16);
-  want_dtype(am, "amax", kF32);
-  want_dim(x, "xp", 2);
+  want_dtype(gth, "gather", kI32);
+  want_dtype(aux, "h_aux", kF32);
+  want_dim(x, "x", 2);
   want_dim(w, "w13", 3);
-  const int64_t rows = x.shape[0], hidden = x.shape[1], e = w.shape[0], inter = w.shape[1] / 2;
+  want_dim(hh, "h", 2);
+  const int64_t x_rows = x.shape[0], hidden = x.shape[1], e = w.shape[0], inter = w.shape[1] / 2;
+  const int64_t rows = hh.shape[0];
   if (w.shape[2] != hidden || w.shape[1] % 2) throw std::runtime_error("w13 must be [E, 2I, H]");
-  if (hh.numel() != rows * inter) throw std::runtime_error("h must be [rows, I]");
+  if (hh.shape[1] != inter) throw std::runtime_error("h must be [rows, I]");
+  if (gth.ptr && gth.numel() != rows) throw std::runtime_error("gather must hold one index per row");
   if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
+  int fmt;
+  if (hh.dtype == kBf16) fmt = HKMOE_BF16;
+  else if (hh.dtype == kF8) fmt = HKMOE_E4M3;
+  else throw std::runtime_error("h: expected bfloat16 or float8_e4m3fn");
   const int mode = scale_mode_of(xs);
   if (mode == HKMOE_SCALE_TENSOR && ws.numel() != e) throw std::runtime_error("w13_scale must be [E]");
   if (mode == HKMOE_SCALE_BLOCK &&
-      (xs.numel() != rows * (hidden / 128) || ws.numel() != e * (2 * inter / 128) * (hidden / 128)))
-    throw std::runtime_error("block scales: xp_scale_t [H/128, rows], w13_scale [E, 2I/128, H/128]");
-  check(hkmoe_grouped_gemm1(x.ptr, static_cast<const float*>(xs.ptr), w.ptr,
-                            static_cast<const float*>(ws.ptr), static_cast<const int32_t*>(o.ptr),
-                            static_cast<const int32_t*>(mo.ptr), rows, static_cast<int32_t>(e),
-                            static_cast<int32_t>(hidden), static_cast<int32_t>(inter), mode, hh.ptr,
-                            static_cast<float*>(am.ptr), current_stream()));
+      (xs.numel() != x_rows * (hidden / 128) || ws.numel() != e * (2 * inter / 128) * (hidden / 128)))
+    throw std::runtime_error("block scales: x_scale [x_rows, H/128], w13_scale [E, 2I/128, H/128]");
+  if (fmt == HKMOE_E4M3 && (!aux.ptr || aux.numel() != rows * (inter / 128)))
+    throw std::runtime_error("e4m3 output needs h_aux [I/128, rows] group scales");
+  check(hkmoe_grouped_gemm1(x.ptr, static_cast<const float*>(xs.ptr), static_cast<const int32_t*>(gth.ptr),
+                            gather_div, x_rows, w.ptr, static_cast<const float*>(ws.ptr),
+                            static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr), rows,
+                            static_cast<int32_t>(e), static_cast<int32_t>(hidden), static_cast<int32_t>(inter),
+                            mode, fmt, hh.ptr, static_cast<float*>(aux.ptr), current_stream()));
 }
 
 void dispatch_requant(py::object h, py::object amax, py::object hq, py::object hs) {

@@ -81,8 +81,11 @@ def moe_forward(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k,
     return out
 
 
-def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k):
-    """The layer one kernel at a time; returns a dict of every intermediate."""
+def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k,
+                      keep_h=False):
+    """The layer one kernel at a time (the same kernels hkmoe_moe_forward
+    enqueues); returns a dict of every intermediate.  With ``keep_h`` the block
+    path also runs GEMM 1 once more with a bf16 output (``h``) for inspection."""
     _check_dev(x_q, logits, w13_q, w2_q)
     dev = x_q.device
     t, hidden = x_q.shape
@@ -99,23 +102,28 @@ def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, to
         counts=torch.empty(e, **i32), offsets=torch.empty(e + 1, **i32),
         mtile_offsets=torch.empty(e + 1, **i32), amax=torch.empty(1, **f32),
         perm=torch.empty(rows, **i32), inv_perm=torch.empty(rows, **i32),
-        xp=torch.empty((rows, hidden), dtype=F8, device=dev),
-        xps=(torch.empty((hidden // GROUP, rows), **f32) if block else x_scale),
-        h=torch.empty((rows, inter), dtype=torch.bfloat16, device=dev),
         hq=torch.empty((rows, inter), dtype=F8, device=dev),
         hs=(torch.empty((inter // GROUP, rows), **f32) if block else torch.empty(1, **f32)),
         y=torch.empty((rows, hidden), dtype=torch.bfloat16, device=dev),
         out=torch.empty((t, hidden), dtype=torch.bfloat16, device=dev),
     )
+    if not block or keep_h:
+        r["h"] = torch.empty((rows, inter), dtype=torch.bfloat16, device=dev)
     tk_kernel.dispatch_route_topk(logits, r["topk_idx"], r["topk_w"], r["block_counts"])
     tk_kernel.dispatch_expert_offsets(r["block_counts"], t, r["counts"], r["offsets"],
                                       r["block_base"], r["mtile_offsets"], r["amax"])
     tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"],
-                               r["inv_perm"], x_q, x_scale if block else None, r["xp"],
-                               r["xps"] if block else None)
-    tk_kernel.dispatch_grouped_gemm1(r["xp"], r["xps"], w13_q, w13_scale, r["offsets"],
-                                     r["mtile_offsets"], r["h"], None if block else r["amax"])
-    tk_kernel.dispatch_requant(r["h"], None if block else r["amax"], r["hq"], r["hs"])
+                               r["inv_perm"], None, None, None, None)
+    if block:
+        tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
+                                         r["offsets"], r["mtile_offsets"], r["hq"], r["hs"])
+        if keep_h:
+            tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
+                                             r["offsets"], r["mtile_offsets"], r["h"], None)
+    else:
+        tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
+                                         r["offsets"], r["mtile_offsets"], r["h"], r["amax"])
+        tk_kernel.dispatch_requant(r["h"], r["amax"], r["hq"], r["hs"])
     tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2_q, w2_scale, r["offsets"],
                                      r["mtile_offsets"], r["y"])
     tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])

@@ -38,7 +38,7 @@ enum hkmoe_status {
   HKMOE_ERR_WORKSPACE = 4
 };
 
-enum hkmoe_dtype { HKMOE_BF16 = 0, HKMOE_F32 = 1 };
+enum hkmoe_dtype { HKMOE_BF16 = 0, HKMOE_F32 = 1, HKMOE_E4M3 = 2 };
 
 enum hkmoe_scale_mode {
   HKMOE_SCALE_TENSOR = 0, /* one fp32 scale per tensor (weights: one per expert) */
@@ -69,8 +69,10 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
  *   Order: descending logit, ties to the lower expert id.  Weights: softmax
  *   over the k selected logits.  block_counts: workspace [nblk, E] int32 with
  *   nblk = hkmoe_route_blocks(T).  E <= 1024, 1 <= k <= min(E, 32).
- * No reference counterpart (the reference has no router; SURVEY of
- * /root/reference finds no top-k/softmax routing code).
+ * The reference has no router, histogram or permutation: the routing entry
+ * points (this one, hkmoe_expert_offsets, hkmoe_scatter) and the MoE entry
+ * points below have no reference counterpart; they follow its binding style
+ * (caller-owned device buffers, one call per kernel as in dispatch_micro).
  */
 int hkmoe_route_blocks(int64_t num_tokens);
 int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_experts, int32_t top_k,
@@ -103,24 +105,33 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
 
 /*
  * Grouped GEMM 1 with fused SiLU(gate)*up:
- *   h[p, i] = bf16( silu(g) * u ),  [g | u] = deq(xp[p]) . deq(W13[e])^T
- *   xp [R,H] e4m3 with R = T*k rows ordered by expert (offsets [E+1]);
- *   w13 [E, 2I, H] e4m3 (gate rows 0..I-1, up rows I..2I-1);
- *   TENSOR: xp_scale [1], w13_scale [E]; the max |h| is accumulated into
- *           *amax (must be zeroed before; hkmoe_expert_offsets can do it).
- *   BLOCK:  xp_scale_t [H/128, R], w13_scale [E, 2I/128, H/128].
- *   Requires H % 128 == 0, I % 128 == 0.
+ *   h[p, i] = bf16( silu(g) * u ),  [g | u] = deq(x[row(p)]) . deq(W13[e])^T
+ *   for every row p of expert e (rows ordered by expert, offsets [E+1]).
+ *   x [x_rows, H] e4m3; row(p) = gather[p] / gather_div when gather != NULL
+ *   (the expert-sorted permutation: token rows are read in place, no permuted
+ *   copy), else row(p) = p.
+ *   w13 [E, 2I, H] e4m3 (gate rows 0..I-1, up rows I..2I-1).
+ *   TENSOR: x_scale [1], w13_scale [E]; out_format must be HKMOE_BF16:
+ *           h bf16 [rows, I], and max|h| is accumulated into h_aux[0] (must be
+ *           zeroed before; hkmoe_expert_offsets can do it; may be NULL).
+ *   BLOCK:  x_scale [x_rows, H/128], w13_scale [E, 2I/128, H/128];
+ *           out_format HKMOE_BF16: h bf16 [rows, I] (h_aux unused), or
+ *           out_format HKMOE_E4M3: the 1x128-group requantisation of that bf16 h
+ *           is fused in: h e4m3 [rows, I], h_aux = group scales [I/128, rows].
+ *   Requires H % 128 == 0, I % 128 == 0, H <= 16384.
  */
-int hkmoe_grouped_gemm1(const void* xp, const float* xp_scale, const void* w13,
+int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gather,
+                        int32_t gather_div, int64_t x_rows, const void* w13,
                         const float* w13_scale, const int32_t* offsets,
                         const int32_t* mtile_offsets, int64_t rows, int32_t num_experts,
-                        int32_t hidden, int32_t inter, int scale_mode, void* h, float* amax,
-                        hkmoe_stream_t stream);
+                        int32_t hidden, int32_t inter, int scale_mode, int out_format, void* h,
+                        float* h_aux, hkmoe_stream_t stream);
 
 /*
- * Requantise the bf16 intermediate to e4m3 for GEMM 2.
+ * Requantise a bf16 intermediate to e4m3 for GEMM 2.
  *   TENSOR: hs[0] = scale(amax), hq = e4m3(h / hs[0]) (amax from GEMM 1).
- *   BLOCK:  1x128 groups, hs_t [I/128, R] (transposed) = amax_g / 448.
+ *   BLOCK:  1x128 groups, hs_t [I/128, R] (transposed) = scale(amax_g).
+ *   scale(a) = max(a / 448, 2^-126), or 1 for a == 0.
  */
 int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, const float* amax,
                   void* hq, float* hs, hkmoe_stream_t stream);

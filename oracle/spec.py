@@ -31,10 +31,14 @@ GROUP = 128
 # ----------------------------------------------------------------------------
 # quantisers
 # ----------------------------------------------------------------------------
+FLT_MIN = np.float32(2.0 ** -126)
+
+
 def scale_from_amax(amax):
-    """s = amax / 448 in fp32, and 1.0 where amax == 0 (all-zero block)."""
+    """s = max(amax / 448, 2^-126) in fp32, and 1.0 where amax == 0 (all-zero
+    block): every scale is a positive normal fp32 number."""
     amax = np.asarray(amax, dtype=np.float32)
-    s = amax / np.float32(E4M3_MAX)
+    s = np.maximum(amax / np.float32(E4M3_MAX), FLT_MIN)
     return np.where(amax > 0, s, np.float32(1.0)).astype(np.float32)
 
 

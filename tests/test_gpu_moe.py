@@ -31,9 +31,9 @@ def _np(t):
     return t.detach().cpu().numpy()
 
 
-def _run_steps(hk, g):
+def _run_steps(hk, g, keep_h=True):
     r = hk.moe_forward_steps(g["x_q"], g["x_scale"], g["logits"], g["w13_q"], g["w13_scale"],
-                             g["w2_q"], g["w2_scale"], g["top_k"])
+                             g["w2_q"], g["w2_scale"], g["top_k"], keep_h=keep_h)
     torch.cuda.synchronize()
     return r
 
@@ -46,7 +46,6 @@ def test_moe_stepwise_parity(hk, name):
     ref = spec.moe_forward(d["x_q"], d["x_scale"], d["logits"], d["w13_q"], d["w13_s"], d["w2_q"],
                            d["w2_s"], d["k"], return_all=True)
     block = SMALL[name]["block"]
-    k = d["k"]
     # routing: bit-exact
     np.testing.assert_array_equal(_np(r["topk_idx"]), ref["topk_idx"])
     assert rel_err(_np(r["topk_w"]), ref["topk_w"]) <= 1e-6
@@ -56,14 +55,12 @@ def test_moe_stepwise_parity(hk, name):
     np.testing.assert_array_equal(_np(r["mtile_offsets"]), mt)
     np.testing.assert_array_equal(_np(r["perm"]), ref["perm"])
     np.testing.assert_array_equal(_np(r["inv_perm"]), ref["inv_perm"])
-    np.testing.assert_array_equal(f8_np(r["xp"]), ref["xp"])
-    if block:
-        np.testing.assert_array_equal(_np(r["xps"]).T, ref["xps"])
-    # GEMM1 + SiLU*up, fed identical inputs: tolerance vs fp32
+    # GEMM1 + SiLU*up (token rows gathered through perm): tolerance vs fp32
     h = bf16_np(r["h"])
     h_ref32 = spec.gemm1_silu(ref["xp"], ref["xps"], d["w13_q"], d["w13_s"], ref["offsets"], rounded=False)
     assert rel_err(h, h_ref32) <= TOL
-    # requant of the GPU's own h: bit-exact
+    # requantisation of the GPU's own bf16 h: bit-exact (block mode: fused into
+    # GEMM 1's epilogue; per-tensor mode: the requant kernel)
     hq_ref, hs_ref = spec.requant(h, block)
     np.testing.assert_array_equal(f8_np(r["hq"]), hq_ref)
     if block:
@@ -78,7 +75,29 @@ def test_moe_stepwise_parity(hk, name):
     assert rel_err(bf16_np(r["out"]), out_ref32) <= TOL
     # end to end against the oracle's own pipeline
     assert rel_err(bf16_np(r["out"]), ref["out_f32"]) <= TOL
-    del k
+
+
+@pytest.mark.parametrize("block", [False, True])
+def test_scatter_row_copy(hk, block):
+    """hkmoe_scatter with x_q: the permuted row copy (and transposed scales) is bit-exact."""
+    d = synth.make_moe(T=70, H=512, I=128, E=12, k=3, block=block, skew=True, seed=4)
+    g = moe_inputs_to_gpu(d)
+    ref = spec.moe_forward(d["x_q"], d["x_scale"], d["logits"], d["w13_q"], d["w13_s"], d["w2_q"],
+                           d["w2_s"], d["k"], return_all=True)
+    t, k, e, hdim = 70, 3, 12, 512
+    r = _run_steps(hk, g, keep_h=False)
+    perm = torch.empty_like(r["perm"])
+    inv = torch.empty_like(r["inv_perm"])
+    xp = torch.empty((t * k, hdim), dtype=torch.float8_e4m3fn, device="cuda")
+    xps = torch.empty((hdim // 128, t * k), dtype=torch.float32, device="cuda") if block else None
+    hk.tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], perm, inv, g["x_q"],
+                                  g["x_scale"] if block else None, xp, xps)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_np(perm), ref["perm"])
+    np.testing.assert_array_equal(f8_np(xp), ref["xp"])
+    if block:
+        np.testing.assert_array_equal(_np(xps).T, ref["xps"])
+    del e
 
 
 @pytest.mark.parametrize("name", ["tensor_e8k2", "block_e16k4_skew"])
@@ -86,7 +105,7 @@ def test_moe_single_call_matches_steps(hk, name):
     """hkmoe_moe_forward (one C call, carved workspace) == the stepwise path, bit for bit."""
     d = synth.make_moe(seed=12, **SMALL[name])
     g = moe_inputs_to_gpu(d)
-    r = _run_steps(hk, g)
+    r = _run_steps(hk, g, keep_h=False)
     out = hk.moe_forward(g["x_q"], g["x_scale"], g["logits"], g["w13_q"], g["w13_scale"],
                          g["w2_q"], g["w2_scale"], g["top_k"])
     torch.cuda.synchronize()
