@@ -67,7 +67,8 @@ int device_cus() {
 }
 
 template <Epi EPI, Scale SC>
-int launch_gemm(const GemmParams& p, hipStream_t stream) {
+int launch_gemm(GemmParams p, hipStream_t stream) {
+  p.a_bytes = static_cast<uint32_t>(std::min<int64_t>(p.a_rows * p.K, 0xffffffffll));
   static bool attr_set[kMaxDevices] = {false};
   int dev = 0;
   (void)hipGetDevice(&dev);
@@ -106,7 +107,7 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
   HK_REQUIRE(a && b && c, "gemm_fp8: null tensor pointer");
   HK_REQUIRE(m >= 0 && n > 0 && k > 0, "gemm_fp8: bad shape M=%lld N=%lld K=%lld", (long long)m,
              (long long)n, (long long)k);
-  HK_REQUIRE(k % kBK == 0, "gemm_fp8: K=%lld must be a multiple of 128", (long long)k);
+  HK_REQUIRE(k % 128 == 0, "gemm_fp8: K=%lld must be a multiple of 128", (long long)k);
   HK_REQUIRE(n % kBN == 0, "gemm_fp8: N=%lld must be a multiple of 256", (long long)n);
   HK_REQUIRE(k <= (1 << 20) && n * k < (1ll << 32) && m < (1ll << 31),
              "gemm_fp8: operand too large for 32-bit buffer offsets");
@@ -203,8 +204,8 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
   HK_REQUIRE(x && w13 && offsets && mtile_offsets && h, "grouped_gemm1: null pointer");
   HK_REQUIRE(x_scale && w13_scale, "grouped_gemm1: null scale pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1: bad E=%d", num_experts);
-  HK_REQUIRE(hidden > 0 && hidden % kBK == 0 && hidden <= kBK * kMaxKBlocks,
-             "grouped_gemm1: hidden=%d must be a multiple of 128 and <= %d", hidden, kBK * kMaxKBlocks);
+  HK_REQUIRE(hidden > 0 && hidden % kGroup == 0 && hidden <= kGroup * kMaxKBlocks,
+             "grouped_gemm1: hidden=%d must be a multiple of 128 and <= %d", hidden, kGroup * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "grouped_gemm1: inter=%d must be a multiple of 128", inter);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm1: bad rows");
   HK_REQUIRE(x_rows >= 1 && x_rows * hidden < (1ll << 32), "grouped_gemm1: x_rows=%lld out of range",
@@ -278,8 +279,8 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
   HK_REQUIRE(hq && hs && w2 && w2_scale && offsets && mtile_offsets && y, "grouped_gemm2: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2: hidden=%d must be a multiple of 256", hidden);
-  HK_REQUIRE(inter > 0 && inter % kBK == 0 && inter <= kBK * kMaxKBlocks,
-             "grouped_gemm2: inter=%d must be a multiple of 128 and <= %d", inter, kBK * kMaxKBlocks);
+  HK_REQUIRE(inter > 0 && inter % kGroup == 0 && inter <= kGroup * kMaxKBlocks,
+             "grouped_gemm2: inter=%d must be a multiple of 128 and <= %d", inter, kGroup * kMaxKBlocks);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm2: bad rows");
   HK_REQUIRE(static_cast<int64_t>(hidden) * inter < (1ll << 32), "grouped_gemm2: expert weight too large");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
@@ -392,8 +393,8 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "moe_forward: E=%d outside [1, %d]",
              num_experts, kMaxExperts);
   HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK, "moe_forward: bad top_k=%d", top_k);
-  HK_REQUIRE(hidden > 0 && hidden % kBN == 0 && hidden <= kBK * kMaxKBlocks,
-             "moe_forward: hidden=%d must be a multiple of 256 and <= %d", hidden, kBK * kMaxKBlocks);
+  HK_REQUIRE(hidden > 0 && hidden % kBN == 0 && hidden <= kGroup * kMaxKBlocks,
+             "moe_forward: hidden=%d must be a multiple of 256 and <= %d", hidden, kGroup * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "moe_forward: inter=%d must be a multiple of 128", inter);
   const bool block = scale_mode == HKMOE_SCALE_BLOCK;
   const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, block);

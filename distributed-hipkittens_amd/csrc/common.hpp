@@ -20,6 +20,7 @@ namespace hkmoe {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define HK_LDS __attribute__((address_space(3)))
 
@@ -45,19 +46,19 @@ __device__ __forceinline__ i32x4 make_srd(const void* base, uint32_t num_bytes) 
   return r;
 }
 
-// One wave instruction: lane i copies 16 bytes from rsrc+voffset into
-// lds_base + 16*i (lds_base must be wave-uniform).
-__device__ __forceinline__ void load_lds_16B(i32x4 rsrc, void* lds_base, int voffset) {
+// One wave instruction: lane i copies 16 bytes from rsrc + voffset + soffset
+// into lds_base + 16*i (lds_base and soffset must be wave-uniform).
+__device__ __forceinline__ void load_lds_16B(i32x4 rsrc, void* lds_base, int voffset, int soffset = 0) {
   hk_raw_buffer_load_lds(rsrc, reinterpret_cast<HK_LDS uint32_t*>(
                                    reinterpret_cast<uintptr_t>(lds_base)),
-                         16, voffset, 0, 0, 0);
+                         16, voffset, soffset, 0, 0);
 }
 
 // Same with 4 bytes per lane (lane i -> lds_base + 4*i).
-__device__ __forceinline__ void load_lds_4B(i32x4 rsrc, void* lds_base, int voffset) {
+__device__ __forceinline__ void load_lds_4B(i32x4 rsrc, void* lds_base, int voffset, int soffset = 0) {
   hk_raw_buffer_load_lds(rsrc, reinterpret_cast<HK_LDS uint32_t*>(
                                    reinterpret_cast<uintptr_t>(lds_base)),
-                         4, voffset, 0, 0, 0);
+                         4, voffset, soffset, 0, 0);
 }
 
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -72,6 +73,13 @@ __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ f32x4 mfma_e4m3_16x16x128(const i32x8& a, const i32x8& b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// D(32x32 fp32) += A(32x64 e4m3) . B(32x64 e4m3)^T: lane l supplies row l % 32
+// and 32 bytes of K (group l / 32) of each operand; output lane l, register
+// r holds D[8*(r/4) + 4*(l/32) + r%4][l % 32].
+__device__ __forceinline__ f32x16 mfma_e4m3_32x32x64(const i32x8& a, const i32x8& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------

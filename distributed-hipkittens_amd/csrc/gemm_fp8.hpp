@@ -7,35 +7,42 @@
 // 256_256_64_32.cpp:32-200).  Design (all new, CDNA4-first):
 //
 //  * block tile 256 (rows of A) x 256 (rows of B) x 128 (K), 8 waves as 2 x 4;
-//    each wave owns a 128 x 64 sub-tile = 8 x 4 MFMA 16x16x128 tiles.
-//  * K step 128 == one scale block.  With 128x128 weight / 1x128 activation
-//    block scales every MFMA of a K step covers exactly one scale block, and the
-//    accumulator is kept in units of the current block's scale product:
+//    each wave owns a 128 x 64 sub-tile = 8 x 4 v_mfma_f32_16x16x128_f8f6f4.
+//  * two LDS stages of 64 KiB (+1 KiB of activation scales) filled by
+//    buffer_load_dwordx4 ... lds (no VGPR staging): 128-byte row segments, i.e.
+//    whole L2 lines per lane octet.
+//  * ping-pong: waves 4-7 (rows 128-255) run half a K step behind waves 0-3
+//    (rows 0-127).  Every wave passes two barriers per K step and each group
+//    one extra barrier at opposite ends of the K loop, so on every SIMD one
+//    wave issues MFMAs while the other reads its fragments from LDS.  Each
+//    group DMAs its own half of A; group 0 also DMAs B one step ahead; every
+//    wave waits for its own DMA (vmcnt) and LDS reads (lgkmcnt) before a
+//    barrier, which is what makes a stage visible / free for the others.
+//  * 16-byte chunk c of LDS row r is stored at c ^ ((r & 7) ^ ((r >> 3) & 1)):
+//    the ds_read_b128 operand reads of 16 consecutive rows are bank-conflict
+//    free whether the LDS serves 8 or 16 lanes per cycle, and the XOR is a lane
+//    constant for every fragment; the swizzle is applied on the global side
+//    because the DMA writes lanes linearly.
+//  * 128x128 weight / 1x128 activation block scales: K step == scale block, so
+//    the accumulator is kept in units of the current block's scale product,
 //        u_k = u_{k-1} * (s_{k-1} / s_k) + P_k,   C = u_last * s_last,
-//    so the promotion is a multiply of the accumulator *before* the MFMA that
-//    reads it (no MFMA -> VALU dependency inside a K step, no partial-sum
-//    registers).  Scales must be positive normal fp32 numbers.
-//  * global -> LDS with buffer_load_dword{,x4} ... lds (no VGPR staging), two
-//    LDS stages of 64 KiB + 1 KiB of activation scales.  Row r of a tile is
-//    XOR-swizzled at 16-byte granularity (chunk c lives at c ^ ((r >> 1) & 7))
-//    so ds_read_b128 operand reads of 16 consecutive rows hit distinct banks;
-//    the swizzle is applied on the global side because the DMA writes lanes
-//    linearly.  Activation scales are gathered by the same DMA into a
-//    lane-major order (8 consecutive floats per lane).
+//    i.e. one multiply of the accumulator before the block's MFMA (no
+//    MFMA -> VALU dependency, no partial-sum registers).  Scales must be
+//    positive normal fp32 numbers (the quantisers floor them at 2^-126).
 //  * optional row gather: A row of output row p is a_gather[p] / gather_div
-//    (the expert-sorted permutation), so GEMM 1 reads token rows directly and
-//    no permuted copy of the activations is ever written.
-//  * MFMA operands are swapped (B tile as src0, A tile as src1) so each lane
-//    owns 4 consecutive output columns of one output row: 8-byte bf16 stores
-//    and one activation scale per lane per 16-row sub-tile.
+//    (the expert-sorted permutation), so GEMM 1 reads token rows in place.
+//  * MFMA operands are swapped (B fragment as src0) so each lane owns 4
+//    consecutive columns of one output row per 16-row sub-tile: one activation
+//    scale per lane per sub-tile and block.
 //  * persistent grid (one 512-thread workgroup per CU); tiles are walked in
-//    groups of 8 M tiles, and workgroup ids are remapped so that the 32
+//    groups of 8 M tiles and workgroup ids are remapped so that the 32
 //    workgroups resident on one XCD (one L2) take 32 consecutive tiles.
 //  * ragged expert segments: the M-tile list comes from a device-side
-//    mtile_offsets[E+1]; sub-tiles with no valid row skip loads and MFMAs.
-//  * fused epilogues: bf16 store, fp32 store, or SiLU(gate)*up with either a
-//    bf16 store + running |h| max (per-tensor requantisation follows) or an
-//    in-tile 1x128-group requantisation to e4m3 + scales (block mode).
+//    mtile_offsets[E+1]; 16-row sub-tiles with no valid row skip their MFMAs.
+//  * fused epilogues, staged through LDS and written as whole rows: bf16 store,
+//    fp32 store, or SiLU(gate)*up with either a bf16 store + running |h| max
+//    (per-tensor requantisation follows) or an in-tile 1x128-group
+//    requantisation to e4m3 + scales (block mode).
 #pragma once
 
 #include "common.hpp"
@@ -57,8 +64,9 @@ struct GemmParams {
   const int32_t* mtile_offsets;// [E+1] M-tile offsets; nullptr = dense
   float* amax;                 // kSiluBf16: running max |h| (uint-ordered), may be null
   int64_t rows;                // output rows (dense: M)
-  int64_t a_rows;              // rows addressable through `a` (buffer bound)
+  int64_t a_rows;              // rows addressable through `a`
   int64_t as_rs, as_ks;        // activation scale strides (row, K block)
+  uint32_t a_bytes;            // buffer bound of `a`: min(a_rows * K, 2^32 - 1)
   int32_t gather_div;
   int32_t num_experts;
   int32_t K;
@@ -69,24 +77,30 @@ struct GemmParams {
 
 constexpr int kBM = 256, kBN = 256, kBK = 128;
 constexpr int kThreads = 512;
-constexpr int kTileBytes = kBM * kBK;                    // 32 KiB per operand
-constexpr int kScaleBytes = kBM * 4;                     // activation scales of one K step
+constexpr int kTileBytes = kBM * kBK;                    // 32 KiB per operand per stage
+constexpr int kScaleBytes = kBM * 4;                     // activation scales of one K block
 constexpr int kStageBytes = 2 * kTileBytes + kScaleBytes;
 constexpr int kMaxKBlocks = 128;                         // K <= 16384
 constexpr int kBsBytes = 2 * kMaxKBlocks * 4;            // weight scales of one tile
-constexpr int kRedBytes = 4 * kBM * 4;                   // epilogue cross-wave row max
-constexpr int kLdsBytes = 2 * kStageBytes + kBsBytes + kRedBytes;
+constexpr int kMainLds = 2 * kStageBytes + kBsBytes;
+// epilogue staging of a bf16 output tile, rows padded by 16 bytes
+constexpr int kCtLdStore = kBN + 8;                      // bf16 elements per staged row
+constexpr int kCtLdSilu = 128 + 8;
+constexpr int kEpiLds = kBM * kCtLdStore * 2;
+constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
 constexpr int kGroupM = 8;
 
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 
-__device__ __forceinline__ int swz_chunk(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+// XOR applied to the 16-byte chunk index of 128-byte LDS row r.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-// Read one 16x128 operand fragment (32 bytes per lane) from a swizzled tile.
-__device__ __forceinline__ i32x8 read_frag(const uint8_t* tile, int row, int half) {
-  const int c0 = swz_chunk(row, 2 * half), c1 = swz_chunk(row, 2 * half + 1);
-  const i32x4 lo = *reinterpret_cast<const i32x4*>(tile + row * kBK + c0 * 16);
-  const i32x4 hi = *reinterpret_cast<const i32x4*>(tile + row * kBK + c1 * 16);
+// One 16x128 operand fragment (32 bytes per lane: row l % 16, K bytes
+// 32*(l/16) .. +31) from a swizzled 128-byte-row tile; `x` = swz(row).
+__device__ __forceinline__ i32x8 read_frag(const uint8_t* tile, int row, int half, int x) {
+  const uint8_t* base = tile + row * kBK;
+  const i32x4 lo = *reinterpret_cast<const i32x4*>(base + ((2 * half) ^ x) * 16);
+  const i32x4 hi = *reinterpret_cast<const i32x4*>(base + ((2 * half + 1) ^ x) * 16);
   i32x8 r;
   r.s0 = lo.x; r.s1 = lo.y; r.s2 = lo.z; r.s3 = lo.w;
   r.s4 = hi.x; r.s5 = hi.y; r.s6 = hi.z; r.s7 = hi.w;
@@ -95,19 +109,27 @@ __device__ __forceinline__ i32x8 read_frag(const uint8_t* tile, int row, int hal
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Position of tile row r in the lane-major activation-scale layout: the lane
-// with l16 = r % 16 of wave-row r / 128 reads its 8 sub-tile scales as 8
-// consecutive floats.
+// Tile row of activation-scale slot s: the lane with l16 = r % 16 of wave-row
+// r / 128 reads its 8 sub-tile scales as 8 consecutive floats.
 __device__ __forceinline__ int scale_slot_row(int slot) {
   const int wm = slot >> 7, w = slot & 127;
   return wm * 128 + (w & 7) * 16 + (w >> 3);
 }
 
+// Wait for this wave's outstanding DMA and LDS reads, then the workgroup
+// barrier; the asm memory clobber keeps the compiler from moving memory
+// operations across it.
+__device__ __forceinline__ void sync_stage() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+__device__ __forceinline__ void sync_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <Epi EPI, Scale SC>
 __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  float* bs_lds = reinterpret_cast<float*>(smem + 2 * kStageBytes);       // [2][kblocks]
-  float* red_lds = reinterpret_cast<float*>(smem + 2 * kStageBytes + kBsBytes);  // [4][256]
+  float* bs_lds = reinterpret_cast<float*>(smem + 2 * kStageBytes);  // [2][k_blocks]
 
   constexpr bool kBlockSc = (SC == Scale::kBlock);
   constexpr bool kSilu = (EPI == Epi::kSiluBf16 || EPI == Epi::kSiluQuant);
@@ -115,32 +137,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int wm = wave >> 2;   // 0..1  -> 128-row half of the tile
-  const int wn = wave & 3;    // 0..3  -> 64-column quarter of the tile
+  const int grp = wave >> 2;  // ping-pong group == 128-row half of the tile
+  const int wg = wave & 3;    // wave within the group == 64-column quarter
   const int l16 = lane & 15;
   const int lg = lane >> 4;   // 0..3
+  const int wave_row0 = grp * 128;
+  const int fx = swz(l16);    // fragment rows are l16 + multiples of 16
 
   const bool dense = (p.offsets == nullptr);
   const int total_mtiles = dense ? static_cast<int>((p.rows + kBM - 1) / kBM)
                                  : __builtin_amdgcn_readfirstlane(p.mtile_offsets[p.num_experts]);
   const int total_tiles = total_mtiles * p.n_tiles;
-  const int k_iters = p.K / kBK;
+  const int k_steps = p.K / kBK;
 
   // XCD-aware virtual id: workgroups are dispatched round-robin over 8 XCDs,
   // so blockIdx % 8 is the XCD; give each XCD a contiguous run of ids.
   const int g = gridDim.x;
-  const int per_xcd = g >> 3;
-  const int vid = (g & 7) == 0 ? (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3) : blockIdx.x;
+  const int vid = (g & 7) == 0 ? (blockIdx.x & 7) * (g >> 3) + (blockIdx.x >> 3) : blockIdx.x;
 
-  const i32x4 a_srd = make_srd(p.a, static_cast<uint32_t>(min<int64_t>(p.a_rows * p.K, 0xffffffffll)));
+  // DMA geometry: wave instruction i of wave wg (in its group) fills 8 LDS rows
+  // 32*i + 8*wg + lane/8 (+ the group's half for A); the lane fetches logical
+  // chunk (lane & 7) ^ swz(row), which lands swizzled.  swz does not depend on i.
+  const int ld_row = 8 * wg + (lane >> 3);
+  const int ld_chunk = (lane & 7) ^ swz(ld_row);
+  const i32x4 a_srd = make_srd(p.a, p.a_bytes);
 
   for (int tile = vid; tile < total_tiles; tile += g) {
     // ---- tile -> (M tile, N tile), grouped by kGroupM M tiles -------------
     const int per_group = kGroupM * p.n_tiles;
-    const int grp = tile / per_group;
-    const int within = tile - grp * per_group;
-    const int gm_size = min(kGroupM, total_mtiles - grp * kGroupM);
-    const int mt_glob = grp * kGroupM + within % gm_size;
+    const int tg = tile / per_group;
+    const int within = tile - tg * per_group;
+    const int gm_size = min(kGroupM, total_mtiles - tg * kGroupM);
+    const int mt_glob = tg * kGroupM + within % gm_size;
     const int nt = within / gm_size;
 
     // ---- M tile -> expert segment ----------------------------------------
@@ -155,258 +183,280 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         if (p.mtile_offsets[mid] <= mt_glob) lo = mid; else hi = mid;
       }
       e = lo;
-      const int seg0 = p.offsets[e], seg1 = p.offsets[e + 1];
-      row0 = seg0 + (mt_glob - p.mtile_offsets[e]) * kBM;
-      valid = min(kBM, seg1 - row0);
+      row0 = p.offsets[e] + (mt_glob - p.mtile_offsets[e]) * kBM;
+      valid = min(kBM, p.offsets[e + 1] - row0);
     }
     e = __builtin_amdgcn_readfirstlane(e);
     row0 = __builtin_amdgcn_readfirstlane(row0);
     valid = __builtin_amdgcn_readfirstlane(valid);
 
-    const uint8_t* b_expert = p.b + static_cast<int64_t>(e) * p.nb * p.K;
-    const i32x4 b_srd = make_srd(b_expert, static_cast<uint32_t>(p.nb) * p.K);
+    const i32x4 b_srd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K,
+                                 static_cast<uint32_t>(p.nb) * p.K);
 
-    // B rows held by this tile: LDS row `r` maps to weight row b_row(r).
-    // kSilu: quarter q (64 rows) = 32 gate rows then the 32 matching up rows.
-    auto b_row = [&](int r) -> int {
-      if constexpr (kSilu) {
-        const int q = r >> 6, w = r & 63;
-        const int col = nt * 128 + q * 32 + (w & 31);
-        return (w < 32) ? col : (p.n_out + col);
-      } else {
-        return nt * kBN + r;
-      }
-    };
-    auto a_row_of = [&](int r) -> int64_t {  // A row feeding output row row0 + r
-      const int rr = row0 + min(r, valid - 1);
-      return p.a_gather ? static_cast<int64_t>(p.a_gather[rr] / p.gather_div) : rr;
-    };
+    // B (group 0 only): LDS row 32*i + ld_row holds weight row b_row0 + boff(i)
+    //   plain: nt*256 + r                       -> boff(i) = 32*i
+    //   SiLU:  quarter q = r >> 6 = i >> 1 holds 32 gate rows (i even) then
+    //          the 32 matching up rows (i odd) -> boff(i) = 32*(i>>1) + (i&1)*I
+    const int b_row0 = kSilu ? nt * 128 + ld_row : nt * kBN + ld_row;
+    const int b_voff = b_row0 * p.K + ld_chunk * 16;
 
-    // Each wave issues 4 A + 4 B wave-loads (8 rows x 128 B each) per K step.
-    // A row groups whose 16-row sub-tile has no valid row are skipped; rows past
-    // `valid` inside a live sub-tile read the last valid row (results dropped).
-    const int ld_row_in_grp = lane >> 3;   // 0..7
-    const int ld_pchunk = lane & 7;        // physical 16-byte chunk in LDS
-    int a_voff[4], b_voff[4];
-    bool a_live[4];
+    // A (own half): LDS row grp*128 + 32*i + ld_row <- A row of output row
+    // row0 + min(r, valid - 1); 16-row sub-tiles past `valid` are not loaded.
+    int a_voff[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int grp8 = i * 8 + wave;       // 0..31 -> rows 8*grp8 .. +7
-      const int r = grp8 * 8 + ld_row_in_grp;
-      const int c = swz_chunk(r, ld_pchunk);
-      a_voff[i] = static_cast<int>(a_row_of(r) * p.K) + c * 16;
-      a_live[i] = ((grp8 * 8) & ~15) < valid;
-      b_voff[i] = b_row(r) * p.K + c * 16;
+      const int rr = row0 + min(wave_row0 + 32 * i + ld_row, valid - 1);
+      const int ar = p.a_gather ? p.a_gather[rr] / p.gather_div : rr;
+      a_voff[i] = ar * p.K + ld_chunk * 16;
     }
-    // activation scales: waves 0..3 each gather 64 of the tile's 256 rows
+    // activation scales of the own half: waves 0,1 of each group gather 64 slots
+    const bool scale_loader = kBlockSc && wg < 2;
     int as_voff = 0;
-    if constexpr (kBlockSc) {
-      const int slot = (wave & 3) * 64 + lane;
-      as_voff = static_cast<int>(a_row_of(scale_slot_row(slot)) * p.as_rs) * 4;
+    if (scale_loader) {
+      const int rr = row0 + min(scale_slot_row(wave_row0 + wg * 64 + lane), valid - 1);
+      const int ar = p.a_gather ? p.a_gather[rr] / p.gather_div : rr;
+      as_voff = static_cast<int>(ar * p.as_rs) * 4;
     }
-    const i32x4 as_srd = kBlockSc ? make_srd(p.a_scale, 0xffffffffu) : i32x4{0, 0, 0, 0};
 
-    auto issue_stage = [&](int kt, int stage) {
-      uint8_t* sa = smem + stage * kStageBytes;
+    // DMA instructions of one K step, in a fixed order: the own A half (4),
+    // B (8, group 0 only), the activation scales (1, waves 0-1 of each group).
+    // They are issued a few at a time between the MFMAs of the first half-step
+    // so that texture-queue stalls overlap queued MFMA work.
+    constexpr int kOpsPerSub = 4;
+    auto issue_op = [&](int kt, int q) {
+      uint8_t* sa = smem + (kt & 1) * kStageBytes;
       uint8_t* sb = sa + kTileBytes;
       const int koff = kt * kBK;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int grp8 = i * 8 + wave;
-        if (a_live[i]) load_lds_16B(a_srd, sa + grp8 * 1024, a_voff[i] + koff);
-        load_lds_16B(b_srd, sb + grp8 * 1024, b_voff[i] + koff);
-      }
-      if constexpr (kBlockSc) {
-        if (wave < 4)
-          load_lds_4B(as_srd, sb + kTileBytes + wave * 256,
-                      as_voff + static_cast<int>(kt * p.as_ks) * 4);
+      if (q < 4) {
+        const int r8 = wave_row0 + 32 * q + 8 * wg;  // first row of this wave load
+        if ((r8 & ~15) < valid) load_lds_16B(a_srd, sa + r8 * kBK, a_voff[q], koff);
+      } else if (q < 12) {
+        if (grp == 0) {
+          const int i = q - 4;
+          const int boff = kSilu ? (32 * (i >> 1) + ((i & 1) ? p.n_out : 0)) : 32 * i;
+          load_lds_16B(b_srd, sb + (32 * i + 8 * wg) * kBK, b_voff, koff + boff * p.K);
+        }
+      } else if (q == 12) {
+        if (scale_loader) {
+          const i32x4 as_srd = make_srd(p.a_scale, 0xffffffffu);
+          load_lds_4B(as_srd, sb + kTileBytes + (wave_row0 + wg * 64) * 4, as_voff,
+                      static_cast<int>(kt * p.as_ks) * 4);
+        }
       }
     };
+    auto issue_step = [&](int kt) {
+#pragma unroll
+      for (int q = 0; q < 13; ++q) issue_op(kt, q);
+    };
 
-    // ---- accumulators -----------------------------------------------------
     f32x4 acc[8][4];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // number of live 16-row sub-tiles for this wave's 128-row half
-    const int wave_row0 = wm * 128;
     const int live_sub = max(0, min(8, (valid - wave_row0 + 15) >> 4));
 
-    __syncthreads();  // previous tile's readers are done with every LDS buffer
+    __syncthreads();  // previous tile is done with every LDS buffer
     if constexpr (kBlockSc) {
-      // weight scales of this tile for every K block: [2][kblocks]
-      const int kblocks = k_iters;
-      const float* bs = p.b_scale + static_cast<int64_t>(e) * (p.nb / kGroup) * kblocks;
-      const int nb0 = kSilu ? nt : 2 * nt;                       // gate / first n block
+      // weight scales of this tile for every K block: [2][k_steps]
+      const float* bs = p.b_scale + static_cast<int64_t>(e) * (p.nb / kGroup) * k_steps;
+      const int nb0 = kSilu ? nt : 2 * nt;                           // gate / first n block
       const int nb1 = kSilu ? (p.n_out / kGroup + nt) : 2 * nt + 1;  // up / second n block
-      for (int t = tid; t < 2 * kblocks; t += kThreads) {
-        const int h = t / kblocks, kb = t - h * kblocks;
-        bs_lds[t] = bs[(h ? nb1 : nb0) * kblocks + kb];
+      for (int t = tid; t < 2 * k_steps; t += kThreads) {
+        const int h = t >= k_steps;
+        bs_lds[t] = bs[(h ? nb1 : nb0) * k_steps + (t - h * k_steps)];
       }
     }
-    issue_stage(0, 0);
+    issue_step(0);
+    if (grp == 1) sync_lds();  // group 1 runs one barrier (half a step) behind
 
-    // which weight-scale half feeds n sub-tile j of this wave
-    // kSilu: j = 0,1 gate, 2,3 up.  Plain: the wave's 64 columns sit in n block
-    // (wn * 64) / 128 of the tile.
-    float s_prev[8][2];
+    // block scales: the accumulator holds sum / (sa_prev[i] * sb_prev[h])
+    float sa_prev[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sa_prev[i] = 1.0f;
+    float sb_prev0 = 1.0f, sb_prev1 = 1.0f;
 
-    for (int kt = 0; kt < k_iters; ++kt) {
-      const int stage = kt & 1;
-      wait_vmem_all();
-      __syncthreads();
-      if (kt + 1 < k_iters) issue_stage(kt + 1, stage ^ 1);
+    for (int kt = 0; kt < k_steps; ++kt) {
+      sync_stage();  // own DMA of step kt done (group 0: also B) -> stage kt visible
+      const bool more = kt + 1 < k_steps;
 
-      const uint8_t* sa = smem + stage * kStageBytes;
+      const uint8_t* sa = smem + (kt & 1) * kStageBytes;
       const uint8_t* sb = sa + kTileBytes;
 
       i32x8 bf[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = read_frag(sb, wn * 64 + j * 16 + l16, lg);
+      for (int j = 0; j < 4; ++j) bf[j] = read_frag(sb, wg * 64 + j * 16 + l16, lg, fx);
 
-      float r_fac[8][2];
+      float r0[8], r1[8];
       if constexpr (kBlockSc) {
-        const float* sc = reinterpret_cast<const float*>(sb + kTileBytes) + wm * 128 + l16 * 8;
+        const float* sc = reinterpret_cast<const float*>(sb + kTileBytes) + wave_row0 + l16 * 8;
         const f32x4 s_lo = *reinterpret_cast<const f32x4*>(sc);
         const f32x4 s_hi = *reinterpret_cast<const f32x4*>(sc + 4);
-        const float sa_v[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
-        float sb_v[2];
+        const float sa_cur[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
+        float sb_cur0, sb_cur1;
         if constexpr (kSilu) {
-          sb_v[0] = bs_lds[kt];
-          sb_v[1] = bs_lds[k_iters + kt];
+          sb_cur0 = bs_lds[kt];
+          sb_cur1 = bs_lds[k_steps + kt];
         } else {
-          sb_v[0] = sb_v[1] = bs_lds[(wn >> 1) * k_iters + kt];
+          sb_cur0 = sb_cur1 = bs_lds[(wg >> 1) * k_steps + kt];
         }
+        const float rb0 = sb_prev0 * __builtin_amdgcn_rcpf(sb_cur0);
+        const float rb1 = sb_prev1 * __builtin_amdgcn_rcpf(sb_cur1);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float s_cur = sa_v[i] * sb_v[h];
-            r_fac[i][h] = (kt == 0) ? 1.0f : s_prev[i][h] * __builtin_amdgcn_rcpf(s_cur);
-            s_prev[i][h] = s_cur;
-          }
+        for (int i = 0; i < 8; ++i) {
+          const float ra = sa_prev[i] * __builtin_amdgcn_rcpf(sa_cur[i]);
+          r0[i] = ra * rb0;
+          r1[i] = ra * rb1;
+          sa_prev[i] = sa_cur[i];
+        }
+        sb_prev0 = sb_cur0;
+        sb_prev1 = sb_cur1;
       }
 
-      i32x8 af_next = read_frag(sa, wave_row0 + l16, lg);
+      i32x8 anext = read_frag(sa, wave_row0 + l16, lg, fx);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
+        if (i == 4) sync_lds();  // mid-step barrier: the other group switches phase
         if (i < live_sub) {
-          const i32x8 af = af_next;
-          if (i + 1 < 8 && i + 1 < live_sub) af_next = read_frag(sa, wave_row0 + (i + 1) * 16 + l16, lg);
+          const i32x8 af = anext;
+          if (i + 1 < live_sub) anext = read_frag(sa, wave_row0 + (i + 1) * 16 + l16, lg, fx);
+          if constexpr (kBlockSc) {
+            if (kt > 0) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            if constexpr (kBlockSc) acc[i][j] *= r_fac[i][kSilu ? (j >> 1) : 0];
-            acc[i][j] = mfma_e4m3_16x16x128(bf[j], af, acc[i][j]);
+              for (int j = 0; j < 4; ++j) acc[i][j] *= (kSilu && j >= 2) ? r1[i] : r0[i];
+            }
           }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma_e4m3_16x16x128(bf[j], af, acc[i][j]);
+        }
+        if (more && i < 4) {
+#pragma unroll
+          for (int q = i * kOpsPerSub; q < (i == 3 ? 13 : (i + 1) * kOpsPerSub); ++q) issue_op(kt + 1, q);
         }
       }
     }
+    if (grp == 0) sync_lds();  // group 0's extra barrier pairs with group 1's first
 
     // ---- epilogue ----------------------------------------------------------
-    // fold the last block's scale product (block) or the per-tensor scales back in
-    float fac[8][2];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if constexpr (kBlockSc)
-          fac[i][h] = s_prev[i][h];
-        else
-          fac[i][h] = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
-      }
+    // lane holds, for sub-tile i and n fragment j, output row wave_row0+16i+l16
+    // and columns 16*j + 4*lg .. +3 of the wave's 64-column quarter
+    float tens = 1.0f;
+    if constexpr (!kBlockSc) tens = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
+    auto fac = [&](int i, int h) -> float {
+      if constexpr (kBlockSc) return sa_prev[i] * (h ? sb_prev1 : sb_prev0);
+      else return tens;
+    };
 
-    if constexpr (kSilu) {
-      // h = bf16(silu(g) * u); lane holds gate/up for columns col..col+3 of row r
-      uint32_t hb[8][2][4];
-      float row_max[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        row_max[i] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float gv = acc[i][j][q] * fac[i][0];
-            const float uv = acc[i][j + 2][q] * fac[i][1];
-            hb[i][j][q] = bf16_rne_bits(silu(gv) * uv);
-            row_max[i] = fmaxf(row_max[i], fabsf(bf16_bits_to_f32(hb[i][j][q])));
-          }
-      }
-      if constexpr (EPI == Epi::kSiluBf16) {
-        float local_max = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int r = wave_row0 + i * 16 + l16;
-          if (i < live_sub && r < valid) {
-            local_max = fmaxf(local_max, row_max[i]);
-            uint16_t* crow = static_cast<uint16_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const int col = nt * 128 + wn * 32 + j * 16 + lg * 4;
-              uint2 v;
-              v.x = hb[i][j][0] | (hb[i][j][1] << 16);
-              v.y = hb[i][j][2] | (hb[i][j][3] << 16);
-              *reinterpret_cast<uint2*>(crow + col) = v;
-            }
-          }
-        }
-        const float m = wave_max(local_max);
-        if (lane == 0 && p.amax != nullptr)
-          atomicMax(reinterpret_cast<unsigned int*>(p.amax), __float_as_uint(m));
-      } else {
-        // 1x128 group requantisation: the tile's 128 intermediate columns of a
-        // row are one group, spread over 4 lane groups x 4 waves.
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float m = row_max[i];
-          m = fmaxf(m, __shfl_xor(m, 16, 64));
-          m = fmaxf(m, __shfl_xor(m, 32, 64));
-          if (lg == 0) red_lds[wn * kBM + wave_row0 + i * 16 + l16] = m;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int r = wave_row0 + i * 16 + l16;
-          if (i < live_sub && r < valid) {
-            const float amax = fmaxf(fmaxf(red_lds[r], red_lds[kBM + r]),
-                                     fmaxf(red_lds[2 * kBM + r], red_lds[3 * kBM + r]));
-            const float s = scale_from_amax(amax);
-            uint8_t* crow = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const int col = nt * 128 + wn * 32 + j * 16 + lg * 4;
-              uint32_t qv = 0;
-#pragma unroll
-              for (int q = 0; q < 4; ++q) qv |= f32_to_e4m3(bf16_bits_to_f32(hb[i][j][q]) / s) << (8 * q);
-              *reinterpret_cast<uint32_t*>(crow + col) = qv;
-            }
-            if (wn == 0 && lg == 0) p.c_scale[static_cast<int64_t>(nt) * p.rows + row0 + r] = s;
-          }
-        }
-      }
-    } else {
+    if constexpr (EPI == Epi::kStoreF32) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int r = wave_row0 + i * 16 + l16;
         if (i < live_sub && r < valid) {
+          const float f = fac(i, 0);
+          float* crow = static_cast<float*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * kBN + wg * 64;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float f = fac[i][0];
-            const int col = nt * kBN + wn * 64 + j * 16 + lg * 4;
-            const int64_t off = static_cast<int64_t>(row0 + r) * p.n_out + col;
-            if constexpr (EPI == Epi::kStoreF32) {
-              float4 v;
-              v.x = acc[i][j][0] * f; v.y = acc[i][j][1] * f;
-              v.z = acc[i][j][2] * f; v.w = acc[i][j][3] * f;
-              *reinterpret_cast<float4*>(static_cast<float*>(p.c) + off) = v;
-            } else {
+            float4 v;
+            v.x = acc[i][j][0] * f; v.y = acc[i][j][1] * f;
+            v.z = acc[i][j][2] * f; v.w = acc[i][j][3] * f;
+            *reinterpret_cast<float4*>(crow + j * 16 + lg * 4) = v;
+          }
+        }
+      }
+    } else {
+      // stage the bf16 tile in LDS, then write whole rows with 16-byte stores
+      constexpr int ld = kSilu ? kCtLdSilu : kCtLdStore;
+      uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
+      __syncthreads();  // every wave is done reading the stages
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i < live_sub) {
+          uint16_t* crow = ct + (wave_row0 + i * 16 + l16) * ld;
+          if constexpr (kSilu) {
+            const float fg = fac(i, 0), fu = fac(i, 1);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              uint32_t hb[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                hb[q] = bf16_rne_bits(silu(acc[i][j][q] * fg) * (acc[i][j + 2][q] * fu));
+              uint2 v;
+              v.x = hb[0] | (hb[1] << 16);
+              v.y = hb[2] | (hb[3] << 16);
+              *reinterpret_cast<uint2*>(crow + wg * 32 + j * 16 + lg * 4) = v;
+            }
+          } else {
+            const float f = fac(i, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
               uint2 v;
               v.x = pack_bf16x2(acc[i][j][0] * f, acc[i][j][1] * f);
               v.y = pack_bf16x2(acc[i][j][2] * f, acc[i][j][3] * f);
-              *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.c) + off) = v;
+              *reinterpret_cast<uint2*>(crow + wg * 64 + j * 16 + lg * 4) = v;
             }
+          }
+        }
+      }
+      __syncthreads();
+      if constexpr (EPI == Epi::kStoreBf16) {
+        // 32 x 16-byte chunks per 256-column row
+        const int c = tid & 31;
+        for (int r = tid >> 5; r < valid; r += kThreads / 32) {
+          const uint4 v = *reinterpret_cast<const uint4*>(ct + r * ld + c * 8);
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out +
+                                    nt * kBN + c * 8) = v;
+        }
+      } else {
+        // two threads per row, 64 columns each
+        const int r = tid >> 1, half = tid & 1;
+        const uint16_t* src = ct + r * ld + half * 64;
+        float m = 0.0f;
+        if (r < valid) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const uint4 v = *reinterpret_cast<const uint4*>(src + u * 8);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(w[q] & 0xffffu)), fabsf(bf16_bits_to_f32(w[q] >> 16))));
+          }
+        }
+        if constexpr (EPI == Epi::kSiluBf16) {
+          if (r < valid) {
+            uint16_t* dst = static_cast<uint16_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * 128 + half * 64;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+              *reinterpret_cast<uint4*>(dst + u * 8) = *reinterpret_cast<const uint4*>(src + u * 8);
+          }
+          m = wave_max(m);
+          if (lane == 0 && p.amax != nullptr)
+            atomicMax(reinterpret_cast<unsigned int*>(p.amax), __float_as_uint(m));
+        } else {
+          // 1x128 group = the row's 128 columns of this tile
+          m = fmaxf(m, __shfl_xor(m, 1, 64));
+          if (r < valid) {
+            const float s = scale_from_amax(m);
+            uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * 128 + half * 64;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              uint32_t qw[4];
+#pragma unroll
+              for (int h2 = 0; h2 < 2; ++h2) {
+                const uint4 v = *reinterpret_cast<const uint4*>(src + u * 16 + h2 * 8);
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                  const uint32_t lo = w[2 * q], hi = w[2 * q + 1];
+                  qw[h2 * 2 + q] = f32_to_e4m3(bf16_bits_to_f32(lo & 0xffffu) / s) |
+                                   (f32_to_e4m3(bf16_bits_to_f32(lo >> 16) / s) << 8) |
+                                   (f32_to_e4m3(bf16_bits_to_f32(hi & 0xffffu) / s) << 16) |
+                                   (f32_to_e4m3(bf16_bits_to_f32(hi >> 16) / s) << 24);
+                }
+              }
+              *reinterpret_cast<uint4*>(dst + u * 16) = uint4{qw[0], qw[1], qw[2], qw[3]};
+            }
+            if (half == 0) p.c_scale[static_cast<int64_t>(nt) * p.rows + row0 + r] = s;
           }
         }
       }
