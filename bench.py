@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="measured HBM bytes per launch (rocprofv3 --pmc summary)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 1 GiB device-to-device copy (counter calibration)")
     return ap.parse_args()
 
 
@@ -113,16 +115,16 @@ def kernel_breakdown(inp, iters=10):
     k = inp["top_k"]
     calls = [
         ("route_topk", lambda: tk_kernel.dispatch_route_topk(inp["logits"], r["topk_idx"], r["topk_w"], r["block_counts"])),
-        ("expert_offsets", lambda: tk_kernel.dispatch_expert_offsets(r["block_counts"], T, r["counts"], r["offsets"], r["block_base"], r["mtile_offsets"], r["amax"])),
+        ("expert_offsets", lambda: tk_kernel.dispatch_expert_offsets(r["block_counts"], T, r["counts"], r["offsets"], r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"])),
         ("scatter", lambda: tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"], r["inv_perm"], None, None, None, None)),
     ]
     if block:
-        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, inp["w13_q"], inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"])))
+        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, inp["w13_q"], inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8])))
     else:
-        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, inp["w13_q"], inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["h"], r["amax"])))
+        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, inp["w13_q"], inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["h"], r["amax"], r["tile_ctr"][:8])))
         calls.append(("requant", lambda: tk_kernel.dispatch_requant(r["h"], r["amax"], r["hq"], r["hs"])))
     calls += [
-        ("grouped_gemm2", lambda: tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], inp["w2_q"], inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"])),
+        ("grouped_gemm2", lambda: tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], inp["w2_q"], inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], r["tile_ctr"][8:])),
         ("combine", lambda: tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])),
     ]
     ev = {name: [] for name, _ in calls}
@@ -214,6 +216,12 @@ def main():
     flops = gemm_flops(cfg)
     value = flops / dt / 1e12
 
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     ms, r = kernel_breakdown(inp)
     rows = cfg["T"] * cfg["k"]
     g1_flops = 2.0 * rows * 2 * cfg["I"] * cfg["H"]

@@ -34,9 +34,15 @@
 //  * MFMA operands are swapped (B fragment as src0) so each lane owns 4
 //    consecutive columns of one output row per 16-row sub-tile: one activation
 //    scale per lane per sub-tile and block.
-//  * persistent grid (one 512-thread workgroup per CU); tiles are walked in
-//    groups of 8 M tiles and workgroup ids are remapped so that the 32
-//    workgroups resident on one XCD (one L2) take 32 consecutive tiles.
+//  * persistent grid (one 512-thread workgroup per CU).  Tiles form blocks of
+//    8 M tiles x 4 N tiles.  With tile counters (grouped GEMMs) every XCD (one
+//    L2; workgroups are dispatched round-robin, so blockIdx % 8) owns the
+//    blocks b = x, x+8, ... and its 32 workgroups pull tiles of those blocks in
+//    order from the XCD's atomic counter, so they keep working on the same
+//    block and share its operand panels in L2 even when tiles differ in cost
+//    (ragged experts); a drained queue steals from the other XCDs' queues.
+//    Without counters (dense GEMM, equal tiles) the same blocks are walked
+//    statically.
 //  * ragged expert segments: the M-tile list comes from a device-side
 //    mtile_offsets[E+1]; 16-row sub-tiles with no valid row skip their MFMAs.
 //  * fused epilogues, staged through LDS and written as whole rows: bf16 store,
@@ -63,6 +69,7 @@ struct GemmParams {
   const int32_t* offsets;      // [E+1] row offsets; nullptr = dense (one segment of `rows`)
   const int32_t* mtile_offsets;// [E+1] M-tile offsets; nullptr = dense
   float* amax;                 // kSiluBf16: running max |h| (uint-ordered), may be null
+  int32_t* tile_ctr;           // optional: 8 zeroed per-XCD tile counters (dynamic schedule)
   int64_t rows;                // output rows (dense: M)
   int64_t a_rows;              // rows addressable through `a`
   int64_t as_rs, as_ks;        // activation scale strides (row, K block)
@@ -87,7 +94,8 @@ constexpr int kMainLds = 2 * kStageBytes + kBsBytes;
 constexpr int kCtLdStore = kBN + 8;                      // bf16 elements per staged row
 constexpr int kCtLdSilu = 128 + 8;
 constexpr int kEpiLds = kBM * kCtLdStore * 2;
-constexpr int kLdsBytes = kMainLds > kEpiLds ? kMainLds : kEpiLds;
+constexpr int kLdsData = kMainLds > kEpiLds ? kMainLds : kEpiLds;
+constexpr int kLdsBytes = kLdsData + 16;                 // + the broadcast slot of the tile queue
 constexpr int kGroupM = 8;
 
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -147,7 +155,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   const bool dense = (p.offsets == nullptr);
   const int total_mtiles = dense ? static_cast<int>((p.rows + kBM - 1) / kBM)
                                  : __builtin_amdgcn_readfirstlane(p.mtile_offsets[p.num_experts]);
-  const int total_tiles = total_mtiles * p.n_tiles;
   const int k_steps = p.K / kBK;
 
   // XCD-aware virtual id: workgroups are dispatched round-robin over 8 XCDs,
@@ -162,14 +169,51 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   const int ld_chunk = (lane & 7) ^ swz(ld_row);
   const i32x4 a_srd = make_srd(p.a, p.a_bytes);
 
-  for (int tile = vid; tile < total_tiles; tile += g) {
-    // ---- tile -> (M tile, N tile), grouped by kGroupM M tiles -------------
-    const int per_group = kGroupM * p.n_tiles;
-    const int tg = tile / per_group;
-    const int within = tile - tg * per_group;
-    const int gm_size = min(kGroupM, total_mtiles - tg * kGroupM);
-    const int mt_glob = tg * kGroupM + within % gm_size;
-    const int nt = within / gm_size;
+  // tile blocks: 8 M tiles x 4 N tiles
+  const int nbn = (p.n_tiles + 3) >> 2;
+  const int nblocks = ((total_mtiles + 7) >> 3) * nbn;
+  int* s_tile = reinterpret_cast<int*>(smem + kLdsData);
+  const int xcd = blockIdx.x & 7;
+  int steal = 0;          // queues visited so far (thread 0 only)
+  int static_j = vid;     // static schedule: next slot index
+
+  while (true) {
+    // ---- next tile: slot j of queue q -> block b = q + 8*(j/32) -----------
+    int mt_glob = -1, nt = 0;
+    if (p.tile_ctr != nullptr) {
+      if (tid == 0) {
+        int t = -1;
+        while (steal < 8 && t < 0) {
+          const int q = (xcd + steal) & 7;
+          const int nslots = q < nblocks ? 32 * ((nblocks - q + 7) >> 3) : 0;
+          const int j = nslots > 0 ? atomicAdd(&p.tile_ctr[q], 1) : nslots;
+          if (j >= nslots) { ++steal; continue; }
+          const int b = q + 8 * (j >> 5), sl = j & 31;
+          const int m = 8 * (b / nbn) + (sl & 7), n = 4 * (b % nbn) + (sl >> 3);
+          if (m < total_mtiles && n < p.n_tiles) t = m * p.n_tiles + n;
+        }
+        *s_tile = t;
+      }
+      __syncthreads();
+      const int t = *s_tile;
+      if (t < 0) break;
+      mt_glob = t / p.n_tiles;
+      nt = t - mt_glob * p.n_tiles;
+    } else {
+      // same blocks, walked statically: vid-th slot of every round of g slots
+      bool found = false;
+      while (!found) {
+        const int j = static_j;
+        static_j += g;
+        const int b = j >> 5, sl = j & 31;
+        if (b >= nblocks) break;
+        const int m = 8 * (b / nbn) + (sl & 7), n = 4 * (b % nbn) + (sl >> 3);
+        if (m < total_mtiles && n < p.n_tiles) { mt_glob = m; nt = n; found = true; }
+      }
+      if (!found) break;
+    }
+    mt_glob = __builtin_amdgcn_readfirstlane(mt_glob);
+    nt = __builtin_amdgcn_readfirstlane(nt);
 
     // ---- M tile -> expert segment ----------------------------------------
     int e = 0, row0 = 0, valid = 0;

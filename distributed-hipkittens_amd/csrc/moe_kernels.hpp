@@ -17,6 +17,7 @@ constexpr int kRouteThreads = 256; // 4 waves, 8 tokens each
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kScanThreads = 1024;
+constexpr int kTileCounters = 16;  // HKMOE_TILE_COUNTERS
 
 __device__ __forceinline__ bool route_better(float av, int ai, float bv, int bi) {
   if (bi < 0) return ai >= 0;
@@ -120,7 +121,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot) {
 __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
     const int32_t* __restrict__ block_counts, int nblk, int num_experts, int e_stride, int parts,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ block_base,
-    int32_t* __restrict__ mtile_offsets, int tile_m, float* amax_reset) {
+    int32_t* __restrict__ mtile_offsets, int tile_m, float* amax_reset, int32_t* tile_counters) {
   __shared__ int part_sum[kScanThreads];
   __shared__ int wave_tot[kScanThreads / 64];
   const int tid = threadIdx.x;
@@ -176,6 +177,7 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
     }
   }
   if (tid == 0 && amax_reset != nullptr) *amax_reset = 0.0f;
+  if (tile_counters != nullptr && tid < kTileCounters) tile_counters[tid] = 0;
 }
 
 // ---------------------------------------------------------------------------

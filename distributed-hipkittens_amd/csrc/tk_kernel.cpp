@@ -141,12 +141,16 @@ void dispatch_route_topk(py::object logits, py::object idx, py::object w, py::ob
 }
 
 void dispatch_expert_offsets(py::object bc, int64_t num_tokens, py::object counts, py::object offsets,
-                             py::object block_base, py::object mtile_offsets, py::object amax) {
+                             py::object block_base, py::object mtile_offsets, py::object amax,
+                             py::object tile_counters) {
   auto b = as_tensor(bc, "block_counts"), c = as_tensor(counts, "counts"),
        o = as_tensor(offsets, "offsets"), bb = as_tensor(block_base, "block_base"),
-       mo = as_tensor(mtile_offsets, "mtile_offsets"), am = as_tensor_opt(amax, "amax");
+       mo = as_tensor(mtile_offsets, "mtile_offsets"), am = as_tensor_opt(amax, "amax"),
+       tc = as_tensor_opt(tile_counters, "tile_counters");
   for (auto* t : {&b, &c, &o, &bb, &mo}) want_dtype(*t, "int tensor", kI32);
   want_dtype(am, "amax", kF32);
+  want_dtype(tc, "tile_counters", kI32);
+  if (tc.ptr && tc.numel() < HKMOE_TILE_COUNTERS) throw std::runtime_error("tile_counters must hold 16 ints");
   const int64_t e = c.numel();
   if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
   if (b.numel() < static_cast<int64_t>(hkmoe_route_blocks(num_tokens)) * e || bb.numel() < b.numel())
@@ -154,7 +158,7 @@ void dispatch_expert_offsets(py::object bc, int64_t num_tokens, py::object count
   check(hkmoe_expert_offsets(static_cast<const int32_t*>(b.ptr), num_tokens, static_cast<int32_t>(e),
                              static_cast<int32_t*>(c.ptr), static_cast<int32_t*>(o.ptr),
                              static_cast<int32_t*>(bb.ptr), static_cast<int32_t*>(mo.ptr),
-                             static_cast<float*>(am.ptr), current_stream()));
+                             static_cast<float*>(am.ptr), static_cast<int32_t*>(tc.ptr), current_stream()));
 }
 
 void dispatch_scatter(py::object idx, py::object offsets, py::object block_base, py::object perm,
@@ -195,11 +199,13 @@ void dispatch_scatter(py::object idx, py::object offsets, py::object block_base,
 
 void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gather, int32_t gather_div,
                             py::object w13, py::object w13s, py::object offsets, py::object mtile_offsets,
-                            py::object h, py::object h_aux) {
+                            py::object h, py::object h_aux, py::object tile_counters) {
   auto x = as_tensor(x_q, "x"), xs = as_tensor(x_scale, "x_scale"), gth = as_tensor_opt(gather, "gather"),
        w = as_tensor(w13, "w13"), ws = as_tensor(w13s, "w13_scale"), o = as_tensor(offsets, "offsets"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), hh = as_tensor(h, "h"),
-       aux = as_tensor_opt(h_aux, "h_aux");
+       aux = as_tensor_opt(h_aux, "h_aux"), tc = as_tensor_opt(tile_counters, "tile_counters");
+  want_dtype(tc, "tile_counters", kI32);
+  if (tc.ptr && tc.numel() < 8) throw std::runtime_error("tile_counters must hold 8 ints");
   want_dtype(x, "x", kF8);
   want_dtype(w, "w13", kF8);
   want_dtype(xs, "x_scale", kF32);
@@ -230,7 +236,8 @@ void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gathe
                             gather_div, x_rows, w.ptr, static_cast<const float*>(ws.ptr),
                             static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr), rows,
                             static_cast<int32_t>(e), static_cast<int32_t>(hidden), static_cast<int32_t>(inter),
-                            mode, fmt, hh.ptr, static_cast<float*>(aux.ptr), current_stream()));
+                            mode, fmt, hh.ptr, static_cast<float*>(aux.ptr), static_cast<int32_t*>(tc.ptr),
+                            current_stream()));
 }
 
 void dispatch_requant(py::object h, py::object amax, py::object hq, py::object hs) {
@@ -253,10 +260,14 @@ void dispatch_requant(py::object h, py::object amax, py::object hq, py::object h
 }
 
 void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::object w2s,
-                            py::object offsets, py::object mtile_offsets, py::object y) {
+                            py::object offsets, py::object mtile_offsets, py::object y,
+                            py::object tile_counters) {
   auto q = as_tensor(hq, "hq"), s = as_tensor(hs, "hs"), w = as_tensor(w2, "w2"),
        ws = as_tensor(w2s, "w2_scale"), o = as_tensor(offsets, "offsets"),
-       mo = as_tensor(mtile_offsets, "mtile_offsets"), yy = as_tensor(y, "y");
+       mo = as_tensor(mtile_offsets, "mtile_offsets"), yy = as_tensor(y, "y"),
+       tc = as_tensor_opt(tile_counters, "tile_counters");
+  want_dtype(tc, "tile_counters", kI32);
+  if (tc.ptr && tc.numel() < 8) throw std::runtime_error("tile_counters must hold 8 ints");
   want_dtype(q, "hq", kF8);
   want_dtype(w, "w2", kF8);
   want_dtype(s, "hs", kF32);
@@ -277,7 +288,7 @@ void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::obj
                             static_cast<const float*>(ws.ptr), static_cast<const int32_t*>(o.ptr),
                             static_cast<const int32_t*>(mo.ptr), rows, static_cast<int32_t>(e),
                             static_cast<int32_t>(hidden), static_cast<int32_t>(inter), mode, yy.ptr,
-                            current_stream()));
+                            static_cast<int32_t*>(tc.ptr), current_stream()));
 }
 
 void dispatch_combine(py::object y, py::object w, py::object inv_perm, py::object out) {
@@ -381,11 +392,18 @@ PYBIND11_MODULE(tk_kernel, m) {
         py::arg("A"), py::arg("B"), py::arg("C"), py::arg("scale_a") = py::none(),
         py::arg("scale_b") = py::none());
   m.def("dispatch_route_topk", &dispatch_route_topk);
-  m.def("dispatch_expert_offsets", &dispatch_expert_offsets);
+  m.def("dispatch_expert_offsets", &dispatch_expert_offsets, py::arg("block_counts"), py::arg("num_tokens"),
+        py::arg("counts"), py::arg("offsets"), py::arg("block_base"), py::arg("mtile_offsets"),
+        py::arg("amax") = py::none(), py::arg("tile_counters") = py::none());
   m.def("dispatch_scatter", &dispatch_scatter);
-  m.def("dispatch_grouped_gemm1", &dispatch_grouped_gemm1);
+  m.def("dispatch_grouped_gemm1", &dispatch_grouped_gemm1, py::arg("x_q"), py::arg("x_scale"), py::arg("gather"),
+        py::arg("gather_div"), py::arg("w13"), py::arg("w13_scale"), py::arg("offsets"),
+        py::arg("mtile_offsets"), py::arg("h"), py::arg("h_aux") = py::none(),
+        py::arg("tile_counters") = py::none());
   m.def("dispatch_requant", &dispatch_requant);
-  m.def("dispatch_grouped_gemm2", &dispatch_grouped_gemm2);
+  m.def("dispatch_grouped_gemm2", &dispatch_grouped_gemm2, py::arg("hq"), py::arg("hs"), py::arg("w2"),
+        py::arg("w2_scale"), py::arg("offsets"), py::arg("mtile_offsets"), py::arg("y"),
+        py::arg("tile_counters") = py::none());
   m.def("dispatch_combine", &dispatch_combine);
   m.def("dispatch_moe", &dispatch_moe);
   m.def("dispatch_quant_group", &dispatch_quant_group);

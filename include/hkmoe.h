@@ -84,11 +84,14 @@ int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_expert
  *   counts [E], offsets [E+1] (exclusive prefix sum, offsets[E] = T*k),
  *   block_base [nblk, E] (rows of expert e routed from earlier blocks),
  *   mtile_offsets [E+1] (prefix sum of ceil(counts/256): the grouped GEMM's
- *   M-tile list), and zeroes *amax_reset when non-NULL.
+ *   M-tile list), and zeroes *amax_reset and the HKMOE_TILE_COUNTERS ints at
+ *   tile_counters when they are non-NULL.
  */
+#define HKMOE_TILE_COUNTERS 16 /* 8 per grouped GEMM: one tile queue per XCD */
 int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
                          int32_t* counts, int32_t* offsets, int32_t* block_base,
-                         int32_t* mtile_offsets, float* amax_reset, hkmoe_stream_t stream);
+                         int32_t* mtile_offsets, float* amax_reset, int32_t* tile_counters,
+                         hkmoe_stream_t stream);
 
 /*
  * Routing step 3: stable scatter into expert-contiguous order.
@@ -118,6 +121,8 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
  *           out_format HKMOE_BF16: h bf16 [rows, I] (h_aux unused), or
  *           out_format HKMOE_E4M3: the 1x128-group requantisation of that bf16 h
  *           is fused in: h e4m3 [rows, I], h_aux = group scales [I/128, rows].
+ *   tile_counters: NULL (static tile order) or 8 zeroed ints, consumed by the
+ *   call (per-XCD tile queues keep ragged tiles L2-local; zero before reuse).
  *   Requires H % 128 == 0, I % 128 == 0, H <= 16384.
  */
 int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gather,
@@ -125,7 +130,7 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
                         const float* w13_scale, const int32_t* offsets,
                         const int32_t* mtile_offsets, int64_t rows, int32_t num_experts,
                         int32_t hidden, int32_t inter, int scale_mode, int out_format, void* h,
-                        float* h_aux, hkmoe_stream_t stream);
+                        float* h_aux, int32_t* tile_counters, hkmoe_stream_t stream);
 
 /*
  * Requantise a bf16 intermediate to e4m3 for GEMM 2.
@@ -139,12 +144,13 @@ int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, co
 /*
  * Grouped GEMM 2:  y[p] = bf16( deq(hq[p]) . deq(W2[e])^T ),  w2 [E, H, I].
  *   TENSOR: hs [1], w2_scale [E];  BLOCK: hs_t [I/128, R], w2_scale [E, H/128, I/128].
+ *   tile_counters: as for hkmoe_grouped_gemm1.
  *   Requires H % 256 == 0, I % 128 == 0.
  */
 int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
                         const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
                         int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
-                        void* y, hkmoe_stream_t stream);
+                        void* y, int32_t* tile_counters, hkmoe_stream_t stream);
 
 /*
  * Top-k weighted unpermute/combine:

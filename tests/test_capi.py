@@ -1,0 +1,128 @@
+"""C ABI and binding checks that need no GPU: the library loads, exports every
+entry point include/hkmoe.h declares, rejects bad arguments on the host
+before touching the device, and sizes the layer workspace as documented."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hkmoe.h")
+LIB = os.path.join(ROOT, "distributed-hipkittens_amd", "libhkmoe.so")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hkmoe_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail("libhkmoe.so is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB)
+    lib.hkmoe_last_error.restype = ctypes.c_char_p
+    lib.hkmoe_moe_workspace_size.restype = ctypes.c_size_t
+    return lib
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 14, names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version(lib):
+    assert lib.hkmoe_version() >= 100
+
+
+def _err(lib):
+    return lib.hkmoe_last_error().decode()
+
+
+def test_gemm_argument_errors_are_host_side(lib):
+    i64 = ctypes.c_int64
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    assert lib.hkmoe_gemm_fp8(None, fake, fake, i64(64), i64(256), i64(128), None, None, 0, None) == 1
+    assert "null" in _err(lib)
+    assert lib.hkmoe_gemm_fp8(fake, fake, fake, i64(64), i64(256), i64(100), None, None, 0, None) == 1
+    assert "multiple of 128" in _err(lib)
+    assert lib.hkmoe_gemm_fp8(fake, fake, fake, i64(64), i64(200), i64(128), None, None, 0, None) == 1
+    assert "multiple of 256" in _err(lib)
+    assert lib.hkmoe_gemm_fp8(fake, fake, fake, i64(64), i64(256), i64(128), None, None, 7, None) == 1
+    assert "out_dtype" in _err(lib)
+
+
+def test_routing_argument_errors(lib):
+    fake = ctypes.c_void_p(0x1000)
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    assert lib.hkmoe_route_topk(fake, i64(16), i32(2000), i32(2), fake, fake, fake, None) == 1
+    assert "E=2000" in _err(lib)
+    assert lib.hkmoe_route_topk(fake, i64(16), i32(8), i32(9), fake, fake, fake, None) == 1
+    assert "top_k=9" in _err(lib)
+    assert lib.hkmoe_route_topk(fake, i64(16), i32(64), i32(33), fake, fake, fake, None) == 1
+    assert lib.hkmoe_combine(fake, fake, fake, i64(4), i32(2), i32(100), fake, None) == 1
+    assert "multiple of 8" in _err(lib)
+
+
+def test_moe_forward_argument_errors(lib):
+    fake = ctypes.c_void_p(0x1000)
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    args = [fake] * 7 + [i64(64), i32(8), i32(2), i32(4096), i32(1024), 0, fake, None, ctypes.c_size_t(0), None]
+    assert lib.hkmoe_moe_forward(*args) == 4  # HKMOE_ERR_WORKSPACE
+    assert "workspace" in _err(lib)
+    args[12] = 2  # bad scale mode
+    assert lib.hkmoe_moe_forward(*args) == 1
+    assert "scale_mode" in _err(lib)
+    args[12] = 0
+    args[10] = i32(4000)  # hidden not a multiple of 256
+    assert lib.hkmoe_moe_forward(*args) == 1
+    assert "hidden=4000" in _err(lib)
+
+
+def test_grouped_gemm_format_errors(lib):
+    fake = ctypes.c_void_p(0x1000)
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    # e4m3 intermediate output is only defined for block scales
+    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, i64(128),
+                                 i32(8), i32(256), i32(128), 0, 2, fake, fake, None, None)
+    assert rc == 1 and "out_format" in _err(lib)
+    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, i64(128),
+                                 i32(8), i32(256), i32(96), 1, 0, fake, fake, None, None)
+    assert rc == 1 and "inter=96" in _err(lib)
+
+
+def _align(x):
+    return (x + 255) // 256 * 256
+
+
+@pytest.mark.parametrize("t,e,k,h,i,block", [(8192, 256, 8, 7168, 2048, True), (4096, 8, 2, 4096, 14336, False),
+                                             (64, 128, 8, 4096, 1536, True), (0, 4, 1, 256, 128, True)])
+def test_workspace_size_formula(lib, t, e, k, h, i, block):
+    r = t * k
+    nblk = (t + 31) // 32
+    parts = [r * 4, r * 4, nblk * e * 4, nblk * e * 4, e * 4, (e + 1) * 4, (e + 1) * 4, 4, 16 * 4, r * 4, r * 4]
+    if not block:
+        parts.append(r * i * 2)
+    parts += [r * i, r * (i // 128) * 4 if block else 4, r * h * 2]
+    want = sum(_align(p) for p in parts)
+    got = lib.hkmoe_moe_workspace_size(ctypes.c_int64(t), ctypes.c_int32(e), ctypes.c_int32(k),
+                                       ctypes.c_int32(h), ctypes.c_int32(i), 1 if block else 0)
+    assert got == want
+
+
+def test_pybind_module_rejects_host_tensors():
+    import sys
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "distributed-hipkittens_amd"))
+    import tk_kernel
+    a = torch.zeros((256, 128), dtype=torch.float8_e4m3fn)
+    c = torch.zeros((256, 256), dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="GPU device"):
+        tk_kernel.dispatch_micro(a, a, c)
+    with pytest.raises(RuntimeError, match="torch.Tensor"):
+        tk_kernel.dispatch_micro(c.numpy(), a, c)
+    assert tk_kernel.route_blocks(8192) == 256

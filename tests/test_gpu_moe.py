@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bf16_np, f8_np, moe_inputs_to_gpu, rel_err, to_f32
+from helpers import bf16_np, f8_np, moe_inputs_to_gpu, rel_err, to_f32, to_f8
 from oracle import spec, synth
 
 pytestmark = pytest.mark.gpu
@@ -199,3 +199,32 @@ def test_quantisers_bit_exact(hk):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(f8_np(q), q_ref)
     assert _np(s)[0] == s_ref
+
+
+def _golden(name):
+    import os
+    return np.load(os.path.join(os.path.dirname(__file__), "golden", name), allow_pickle=False)
+
+
+@pytest.mark.parametrize("name", ["moe_tensor_e4k2.npz", "moe_block_e8k3_skew.npz", "moe_block_t8_e12k8.npz"])
+def test_golden_fixture_native(hk, name):
+    """The native path on the committed fixtures: routing bit-exact, output <= 1e-2."""
+    g = _golden(name)
+    block = g["x_scale"].ndim == 2
+    d = dict(x_q=g["x_q"], x_scale=g["x_scale"] if block else np.float32(g["x_scale"]), logits=g["logits"],
+             w13_q=g["w13_q"], w13_s=g["w13_s"], w2_q=g["w2_q"], w2_s=g["w2_s"], k=int(g["k"]))
+    gg = moe_inputs_to_gpu(d)
+    r = _run_steps(hk, gg, keep_h=False)
+    np.testing.assert_array_equal(_np(r["topk_idx"]), g["topk_idx"])
+    np.testing.assert_array_equal(_np(r["offsets"]), g["offsets"])
+    np.testing.assert_array_equal(_np(r["perm"]), g["perm"])
+    np.testing.assert_array_equal(_np(r["inv_perm"]), g["inv_perm"])
+    assert rel_err(_np(r["topk_w"]), g["topk_w"]) <= 1e-6
+    assert rel_err(bf16_np(r["out"]), g["out"].astype(np.float32)) <= TOL
+
+
+def test_golden_dense_native(hk):
+    g = _golden("dense_m64_n256_k256.npz")
+    c = hk.gemm_fp8(to_f8(g["a_q"]), to_f8(g["b_q"]), to_f32([g["sa"]]), to_f32([g["sb"]]), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_err(c.cpu().numpy(), g["c_f32"]) <= 1e-4  # fp32 out: scale applied after vs before the sum
