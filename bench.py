@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="measured HBM bytes per launch (rocprofv3 --pmc summary)")
+    ap.add_argument("--weights", default="packed", choices=["packed", "rows"],
+                    help="expert weight layout: packed once at layer construction (default) or row-major")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (counter calibration)")
     return ap.parse_args()
@@ -102,14 +104,16 @@ def gemm_flops(cfg):
     return 2.0 * rows * (2 * cfg["I"]) * cfg["H"] + 2.0 * rows * cfg["H"] * cfg["I"]
 
 
-def kernel_breakdown(inp, iters=10):
+def kernel_breakdown(inp, layer, iters=10):
     """Average ms of each kernel of the stepwise layer, events on torch's current
     stream (the stream every dispatch_* call launches on)."""
     import torch
     import tk_kernel
     import hkmoe
-    r = hkmoe.moe_forward_steps(inp["x_q"], inp["x_scale"], inp["logits"], inp["w13_q"],
-                                inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"])
+    pk = layer.packed
+    w13, w2 = layer.w13_q, layer.w2_q
+    r = hkmoe.moe_forward_steps(inp["x_q"], inp["x_scale"], inp["logits"], w13,
+                                inp["w13_scale"], w2, inp["w2_scale"], inp["top_k"], packed=pk)
     block = inp["x_scale"].dim() == 2
     T = inp["x_q"].shape[0]
     k = inp["top_k"]
@@ -119,12 +123,12 @@ def kernel_breakdown(inp, iters=10):
         ("scatter", lambda: tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"], r["inv_perm"], None, None, None, None)),
     ]
     if block:
-        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, inp["w13_q"], inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8])))
+        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8], packed=pk)))
     else:
-        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, inp["w13_q"], inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["h"], r["amax"], r["tile_ctr"][:8])))
+        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["h"], r["amax"], r["tile_ctr"][:8], packed=pk)))
         calls.append(("requant", lambda: tk_kernel.dispatch_requant(r["h"], r["amax"], r["hq"], r["hs"])))
     calls += [
-        ("grouped_gemm2", lambda: tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], inp["w2_q"], inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], r["tile_ctr"][8:])),
+        ("grouped_gemm2", lambda: tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2, inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], r["tile_ctr"][8:], packed=pk)),
         ("combine", lambda: tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])),
     ]
     ev = {name: [] for name, _ in calls}
@@ -203,7 +207,8 @@ def main():
     torch.cuda.set_device(dev)
     cfg = CONFIGS[args.config]
     inp = make_inputs(cfg, args.seed, dev)
-    layer = hkmoe.MoELayer(inp["w13_q"], inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"])
+    layer = hkmoe.MoELayer(inp["w13_q"], inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"],
+                           pack=args.weights == "packed")
     out = torch.empty((cfg["T"], cfg["H"]), dtype=torch.bfloat16, device=dev)
     for _ in range(args.warmup):
         layer(inp["x_q"], inp["x_scale"], inp["logits"], out=out)
@@ -222,7 +227,7 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    ms, r = kernel_breakdown(inp)
+    ms, r = kernel_breakdown(inp, layer)
     rows = cfg["T"] * cfg["k"]
     g1_flops = 2.0 * rows * 2 * cfg["I"] * cfg["H"]
     g1_tflops = g1_flops / (ms["grouped_gemm1"] * 1e-3) / 1e12
@@ -243,6 +248,7 @@ def main():
                    "inter": cfg["I"], "experts": cfg["E"], "top_k": cfg["k"],
                    "scales": "128x128 weight / 1x128 activation blocks" if cfg["block"] else "per-tensor",
                    "routing": "zipf(1.1) skew" if cfg["skew"] else "N(0,1) logits",
+                   "weights": args.weights,
                    "active_experts": int((counts > 0).sum()), "max_rows": int(counts.max())},
         "pct_fp8_peak": round(100.0 * value / PEAK_FP8_TFLOPS, 2),
         "roofline": {"bound": "mfma", "kernel": "grouped_gemm1 (gate/up + SiLU*up)",

@@ -98,7 +98,7 @@ int pow2_at_least(int v) {
 
 extern "C" {
 
-int hkmoe_version(void) { return 100; }
+int hkmoe_version(void) { return 200; }
 
 const char* hkmoe_last_error(void) { return g_last_error.c_str(); }
 
@@ -202,8 +202,8 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
                         int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
                         const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
                         int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
-                        int out_format, void* h, float* h_aux, int32_t* tile_counters,
-                        hkmoe_stream_t stream) {
+                        int w_layout, int out_format, void* h, float* h_aux,
+                        int32_t* tile_counters, hkmoe_stream_t stream) {
   HK_REQUIRE(x && w13 && offsets && mtile_offsets && h, "grouped_gemm1: null pointer");
   HK_REQUIRE(x_scale && w13_scale, "grouped_gemm1: null scale pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1: bad E=%d", num_experts);
@@ -218,6 +218,8 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
   HK_REQUIRE(2ll * inter * hidden < (1ll << 32), "grouped_gemm1: expert weight too large");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
              "grouped_gemm1: bad scale_mode %d", scale_mode);
+  HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "grouped_gemm1: bad w_layout %d",
+             w_layout);
   HK_REQUIRE(out_format == HKMOE_BF16 || (out_format == HKMOE_E4M3 && scale_mode == HKMOE_SCALE_BLOCK),
              "grouped_gemm1: out_format %d not supported with scale_mode %d", out_format, scale_mode);
   HK_REQUIRE(out_format != HKMOE_E4M3 || h_aux != nullptr, "grouped_gemm1: e4m3 output needs h_aux scales");
@@ -241,6 +243,7 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
   p.nb = 2 * inter;
   p.n_out = inter;
   p.n_tiles = inter / 128;
+  p.b_packed = w_layout == HKMOE_W_PACKED;
   p.tile_ctr = tile_counters;
   auto s = static_cast<hipStream_t>(stream);
   if (scale_mode == HKMOE_SCALE_TENSOR) {
@@ -278,8 +281,8 @@ int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, co
 
 int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
                         const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
-                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode, void* y,
-                        int32_t* tile_counters, hkmoe_stream_t stream) {
+                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
+                        int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream) {
   HK_REQUIRE(hq && hs && w2 && w2_scale && offsets && mtile_offsets && y, "grouped_gemm2: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2: hidden=%d must be a multiple of 256", hidden);
@@ -289,6 +292,8 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
   HK_REQUIRE(static_cast<int64_t>(hidden) * inter < (1ll << 32), "grouped_gemm2: expert weight too large");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
              "grouped_gemm2: bad scale_mode %d", scale_mode);
+  HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "grouped_gemm2: bad w_layout %d",
+             w_layout);
   if (rows == 0) return HKMOE_OK;
   GemmParams p{};
   p.a = static_cast<const uint8_t*>(hq);
@@ -307,10 +312,30 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
   p.nb = hidden;
   p.n_out = hidden;
   p.n_tiles = hidden / kBN;
+  p.b_packed = w_layout == HKMOE_W_PACKED;
   p.tile_ctr = tile_counters;
   auto s = static_cast<hipStream_t>(stream);
   return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kStoreBf16, Scale::kBlock>(p, s)
                                          : launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s);
+}
+
+int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k, int32_t gate_up,
+                       void* packed, hkmoe_stream_t stream) {
+  HK_REQUIRE(w && packed, "pack_weights: null pointer");
+  HK_REQUIRE(w != packed, "pack_weights: in-place packing is not supported");
+  HK_REQUIRE(num_experts >= 0 && n > 0 && n % kBN == 0 && k > 0 && k % kBK == 0,
+             "pack_weights: N=%lld must be a multiple of 256 and K=%lld of 128", (long long)n,
+             (long long)k);
+  HK_REQUIRE(n * k < (1ll << 32) && k <= kBK * kMaxKBlocks, "pack_weights: expert weight too large");
+  HK_REQUIRE(gate_up == 0 || (gate_up > 0 && n == 2ll * gate_up),
+             "pack_weights: gate_up=%d must be 0 or N/2", gate_up);
+  const int64_t chunks = num_experts * n * k / 16;
+  if (chunks == 0) return HKMOE_OK;
+  const int grid = static_cast<int>(std::min<int64_t>((chunks + 255) / 256, 8 * 1024));
+  hipLaunchKernelGGL(pack_weights_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint8_t*>(w), n, static_cast<int>(k), gate_up,
+                     static_cast<uint8_t*>(packed), chunks);
+  return check_launch("pack_weights_kernel");
 }
 
 int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, int64_t num_tokens,
@@ -390,12 +415,14 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
 int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
                       const float* w13_scale, const void* w2, const float* w2_scale,
                       int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
-                      int32_t inter, int scale_mode, void* out, void* workspace,
+                      int32_t inter, int scale_mode, int w_layout, void* out, void* workspace,
                       size_t workspace_bytes, hkmoe_stream_t stream) {
   HK_REQUIRE(x_q && x_scale && logits && w13 && w13_scale && w2 && w2_scale && out,
              "moe_forward: null pointer");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
              "moe_forward: bad scale_mode %d", scale_mode);
+  HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "moe_forward: bad w_layout %d",
+             w_layout);
   HK_REQUIRE(num_tokens >= 0 && num_tokens * top_k < (1ll << 31), "moe_forward: bad T");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "moe_forward: E=%d outside [1, %d]",
              num_experts, kMaxExperts);
@@ -424,15 +451,15 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
     // intermediate and its 1x128 group scales directly.
     HK_TRY(hkmoe_grouped_gemm1(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                                w.mtile_offsets, rows, num_experts, hidden, inter, scale_mode,
-                               HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream));
+                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream));
   } else {
     HK_TRY(hkmoe_grouped_gemm1(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                                w.mtile_offsets, rows, num_experts, hidden, inter, scale_mode,
-                               HKMOE_BF16, w.h, w.amax, w.tile_ctr, stream));
+                               w_layout, HKMOE_BF16, w.h, w.amax, w.tile_ctr, stream));
     HK_TRY(hkmoe_requant(w.h, rows, inter, scale_mode, w.amax, w.hq, w.hs, stream));
   }
   HK_TRY(hkmoe_grouped_gemm2(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, rows, num_experts,
-                             hidden, inter, scale_mode, w.y, w.tile_ctr + 8, stream));
+                             hidden, inter, scale_mode, w_layout, w.y, w.tile_ctr + 8, stream));
   HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
   return HKMOE_OK;
 }

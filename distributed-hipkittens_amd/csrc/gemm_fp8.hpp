@@ -61,7 +61,7 @@ enum class Scale : int { kTensor = 0, kBlock = 1 };
 struct GemmParams {
   const uint8_t* a;            // A rows [a_rows, K] e4m3
   const int32_t* a_gather;     // optional: A row of output row p = a_gather[p] / gather_div
-  const uint8_t* b;            // [E, nb, K] e4m3
+  const uint8_t* b;            // [E, nb, K] e4m3, row-major or packed (b_packed)
   void* c;                     // [rows, n_out]: bf16, fp32 or (kSiluQuant) e4m3
   const float* a_scale;        // kTensor: [1] or null (1.0); kBlock: a_scale[r*as_rs + kb*as_ks]
   const float* b_scale;        // kTensor: [E] or null (1.0); kBlock: [E, nb/128, K/128]
@@ -80,6 +80,7 @@ struct GemmParams {
   int32_t nb;                  // B rows per expert (N, or 2I for the fused gate/up GEMM)
   int32_t n_out;               // output columns (N, or I)
   int32_t n_tiles;             // N tiles per M tile
+  int32_t b_packed;            // 1: b is in the packed tile layout of pack_weights_kernel
 };
 
 constexpr int kBM = 256, kBN = 256, kBK = 128;
@@ -234,15 +235,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     row0 = __builtin_amdgcn_readfirstlane(row0);
     valid = __builtin_amdgcn_readfirstlane(valid);
 
-    const i32x4 b_srd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K,
-                                 static_cast<uint32_t>(p.nb) * p.K);
-
     // B (group 0 only): LDS row 32*i + ld_row holds weight row b_row0 + boff(i)
     //   plain: nt*256 + r                       -> boff(i) = 32*i
     //   SiLU:  quarter q = r >> 6 = i >> 1 holds 32 gate rows (i even) then
     //          the 32 matching up rows (i odd) -> boff(i) = 32*(i>>1) + (i&1)*I
-    const int b_row0 = kSilu ? nt * 128 + ld_row : nt * kBN + ld_row;
-    const int b_voff = b_row0 * p.K + ld_chunk * 16;
+    // Row-major weights: lane offset of that row and chunk, K step kt at byte
+    // kt*128.  Packed weights: the tile's K step kt is the 32 KiB stage image
+    // at kt*32 KiB of the tile's own panel, so instruction i of wave wg reads
+    // the 1 KiB at (32*i + 8*wg)*128 linearly.
+    i32x4 b_srd;
+    int b_voff, b_kstride;
+    if (p.b_packed) {
+      b_srd = make_srd(p.b + (static_cast<int64_t>(e) * (p.nb / kBN) + nt) * kBN * p.K,
+                       static_cast<uint32_t>(kBN) * p.K);
+      b_voff = wg * 8 * kBK + lane * 16;
+      b_kstride = kTileBytes;
+    } else {
+      b_srd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K, static_cast<uint32_t>(p.nb) * p.K);
+      const int b_row0 = kSilu ? nt * 128 + ld_row : nt * kBN + ld_row;
+      b_voff = b_row0 * p.K + ld_chunk * 16;
+      b_kstride = kBK;
+    }
 
     // A (own half): LDS row grp*128 + 32*i + ld_row <- A row of output row
     // row0 + min(r, valid - 1); 16-row sub-tiles past `valid` are not loaded.
@@ -278,7 +291,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         if (grp == 0) {
           const int i = q - 4;
           const int boff = kSilu ? (32 * (i >> 1) + ((i & 1) ? p.n_out : 0)) : 32 * i;
-          load_lds_16B(b_srd, sb + (32 * i + 8 * wg) * kBK, b_voff, koff + boff * p.K);
+          const int ioff = p.b_packed ? 32 * i * kBK : boff * p.K;
+          load_lds_16B(b_srd, sb + (32 * i + 8 * wg) * kBK, b_voff, kt * b_kstride + ioff);
         }
       } else if (q == 12) {
         if (scale_loader) {
@@ -505,6 +519,37 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         }
       }
     }
+  }
+}
+
+// Packed weight layout (a load-time transform; the grouped GEMMs then stream
+// every weight panel sequentially instead of 128 bytes from each of 256 rows
+// 7-14 KiB apart): for expert e, 256-row N tile nt and K step kt,
+//   packed[((e*(nb/256) + nt)*(K/128) + kt)*32 KiB + R*128 + P*16 + b]
+//     = w[e][wrow(R)][kt*128 + (P ^ swz(R))*16 + b],
+// i.e. the byte image of the GEMM's B stage.  wrow(R) = nt*256 + R, or with
+// gate_up = I (fused gate/up weights [gate I rows | up I rows]) the 64-row
+// quarter R>>6 holds 32 gate rows then the 32 matching up rows:
+//   wrow(R) = nt*128 + 32*(R>>6) + (R&31) + ((R>>5)&1)*I.
+// One thread moves one 16-byte chunk; writes are linear.
+__global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __restrict__ w, int64_t nb,
+                                                           int K, int gate_up, uint8_t* __restrict__ out,
+                                                           int64_t chunks) {
+  const int ks = K / kBK;
+  const int64_t ntile = nb / kBN;
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < chunks;
+       c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t blk = c >> 11;  // 2048 chunks per 32 KiB stage image
+    const int in = static_cast<int>(c & 2047);
+    const int R = in >> 3, P = in & 7;
+    const int kt = static_cast<int>(blk % ks);
+    const int64_t tile = blk / ks;
+    const int64_t e = tile / ntile;
+    const int nt = static_cast<int>(tile - e * ntile);
+    const int64_t wrow = gate_up ? nt * 128 + 32 * (R >> 6) + (R & 31) + ((R >> 5) & 1) * gate_up
+                                 : static_cast<int64_t>(nt) * kBN + R;
+    const uint8_t* src = w + (e * nb + wrow) * K + kt * kBK + ((P ^ swz(R)) << 4);
+    *reinterpret_cast<uint4*>(out + (c << 4)) = *reinterpret_cast<const uint4*>(src);
   }
 }
 

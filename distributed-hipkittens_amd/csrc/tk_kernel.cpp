@@ -199,7 +199,7 @@ void dispatch_scatter(py::object idx, py::object offsets, py::object block_base,
 
 void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gather, int32_t gather_div,
                             py::object w13, py::object w13s, py::object offsets, py::object mtile_offsets,
-                            py::object h, py::object h_aux, py::object tile_counters) {
+                            py::object h, py::object h_aux, py::object tile_counters, bool packed) {
   auto x = as_tensor(x_q, "x"), xs = as_tensor(x_scale, "x_scale"), gth = as_tensor_opt(gather, "gather"),
        w = as_tensor(w13, "w13"), ws = as_tensor(w13s, "w13_scale"), o = as_tensor(offsets, "offsets"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), hh = as_tensor(h, "h"),
@@ -236,8 +236,8 @@ void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gathe
                             gather_div, x_rows, w.ptr, static_cast<const float*>(ws.ptr),
                             static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr), rows,
                             static_cast<int32_t>(e), static_cast<int32_t>(hidden), static_cast<int32_t>(inter),
-                            mode, fmt, hh.ptr, static_cast<float*>(aux.ptr), static_cast<int32_t*>(tc.ptr),
-                            current_stream()));
+                            mode, packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, fmt, hh.ptr,
+                            static_cast<float*>(aux.ptr), static_cast<int32_t*>(tc.ptr), current_stream()));
 }
 
 void dispatch_requant(py::object h, py::object amax, py::object hq, py::object hs) {
@@ -261,7 +261,7 @@ void dispatch_requant(py::object h, py::object amax, py::object hq, py::object h
 
 void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::object w2s,
                             py::object offsets, py::object mtile_offsets, py::object y,
-                            py::object tile_counters) {
+                            py::object tile_counters, bool packed) {
   auto q = as_tensor(hq, "hq"), s = as_tensor(hs, "hs"), w = as_tensor(w2, "w2"),
        ws = as_tensor(w2s, "w2_scale"), o = as_tensor(offsets, "offsets"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), yy = as_tensor(y, "y"),
@@ -287,8 +287,9 @@ void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::obj
   check(hkmoe_grouped_gemm2(q.ptr, static_cast<const float*>(s.ptr), w.ptr,
                             static_cast<const float*>(ws.ptr), static_cast<const int32_t*>(o.ptr),
                             static_cast<const int32_t*>(mo.ptr), rows, static_cast<int32_t>(e),
-                            static_cast<int32_t>(hidden), static_cast<int32_t>(inter), mode, yy.ptr,
-                            static_cast<int32_t*>(tc.ptr), current_stream()));
+                            static_cast<int32_t>(hidden), static_cast<int32_t>(inter), mode,
+                            packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, yy.ptr, static_cast<int32_t*>(tc.ptr),
+                            current_stream()));
 }
 
 void dispatch_combine(py::object y, py::object w, py::object inv_perm, py::object out) {
@@ -313,7 +314,7 @@ size_t moe_workspace_size(int64_t t, int32_t e, int32_t k, int32_t hidden, int32
 
 void dispatch_moe(py::object x_q, py::object x_scale, py::object logits, py::object w13,
                   py::object w13s, py::object w2, py::object w2s, int32_t top_k, py::object out,
-                  py::object workspace) {
+                  py::object workspace, bool packed) {
   auto x = as_tensor(x_q, "x_q"), xs = as_tensor(x_scale, "x_scale"), l = as_tensor(logits, "logits"),
        a = as_tensor(w13, "w13"), as = as_tensor(w13s, "w13_scale"), b = as_tensor(w2, "w2"),
        bs = as_tensor(w2s, "w2_scale"), o = as_tensor(out, "out"), ws = as_tensor(workspace, "workspace");
@@ -342,7 +343,20 @@ void dispatch_moe(py::object x_q, py::object x_scale, py::object logits, py::obj
   check(hkmoe_moe_forward(x.ptr, static_cast<const float*>(xs.ptr), static_cast<const float*>(l.ptr), a.ptr,
                           static_cast<const float*>(as.ptr), b.ptr, static_cast<const float*>(bs.ptr), t,
                           static_cast<int32_t>(e), top_k, static_cast<int32_t>(hidden),
-                          static_cast<int32_t>(inter), mode, o.ptr, ws.ptr, bytes, current_stream()));
+                          static_cast<int32_t>(inter), mode, packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, o.ptr,
+                          ws.ptr, bytes, current_stream()));
+}
+
+// Load-time packing of expert weights [E, N, K] into the grouped GEMMs' tile
+// layout (same shape and size; pass packed=True to the GEMMs afterwards).
+void dispatch_pack_weights(py::object w, py::object packed, int32_t gate_up) {
+  auto src = as_tensor(w, "w"), dst = as_tensor(packed, "packed");
+  want_dtype(src, "w", kF8);
+  want_dtype(dst, "packed", kF8);
+  want_dim(src, "w", 3);
+  if (dst.shape != src.shape) throw std::runtime_error("packed must have the shape of w");
+  check(hkmoe_pack_weights(src.ptr, src.shape[0], src.shape[1], src.shape[2], gate_up, dst.ptr,
+                           current_stream()));
 }
 
 void dispatch_quant_group(py::object x, py::object q, py::object s) {
@@ -399,13 +413,16 @@ PYBIND11_MODULE(tk_kernel, m) {
   m.def("dispatch_grouped_gemm1", &dispatch_grouped_gemm1, py::arg("x_q"), py::arg("x_scale"), py::arg("gather"),
         py::arg("gather_div"), py::arg("w13"), py::arg("w13_scale"), py::arg("offsets"),
         py::arg("mtile_offsets"), py::arg("h"), py::arg("h_aux") = py::none(),
-        py::arg("tile_counters") = py::none());
+        py::arg("tile_counters") = py::none(), py::arg("packed") = false);
   m.def("dispatch_requant", &dispatch_requant);
   m.def("dispatch_grouped_gemm2", &dispatch_grouped_gemm2, py::arg("hq"), py::arg("hs"), py::arg("w2"),
         py::arg("w2_scale"), py::arg("offsets"), py::arg("mtile_offsets"), py::arg("y"),
-        py::arg("tile_counters") = py::none());
+        py::arg("tile_counters") = py::none(), py::arg("packed") = false);
   m.def("dispatch_combine", &dispatch_combine);
-  m.def("dispatch_moe", &dispatch_moe);
+  m.def("dispatch_moe", &dispatch_moe, py::arg("x_q"), py::arg("x_scale"), py::arg("logits"), py::arg("w13"),
+        py::arg("w13_scale"), py::arg("w2"), py::arg("w2_scale"), py::arg("top_k"), py::arg("out"),
+        py::arg("workspace"), py::arg("packed") = false);
+  m.def("dispatch_pack_weights", &dispatch_pack_weights, py::arg("w"), py::arg("packed"), py::arg("gate_up"));
   m.def("dispatch_quant_group", &dispatch_quant_group);
   m.def("dispatch_quant_block", &dispatch_quant_block);
   m.def("dispatch_quant_tensor", &dispatch_quant_tensor);

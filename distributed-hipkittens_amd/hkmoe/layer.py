@@ -64,9 +64,23 @@ def gemm_fp8(a_q, b_q, scale_a=None, scale_b=None, out_dtype=torch.bfloat16):
 # ----------------------------------------------------------------------------
 # the layer
 # ----------------------------------------------------------------------------
+def pack_weights(w_q, gate_up=False):
+    """Load-time repack of e4m3 expert weights [E, N, K] into the grouped
+    GEMMs' tile layout (hkmoe_pack_weights); same shape, new tensor.  Pass
+    ``gate_up=True`` for the fused gate/up weights [E, 2I, H] of GEMM 1."""
+    _check_dev(w_q)
+    if w_q.dtype != F8 or w_q.dim() != 3:
+        raise RuntimeError("pack_weights: expected float8_e4m3fn [E, N, K]")
+    w_q = w_q.contiguous()
+    packed = torch.empty_like(w_q)
+    tk_kernel.dispatch_pack_weights(w_q, packed, w_q.shape[1] // 2 if gate_up else 0)
+    return packed
+
+
 def moe_forward(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k,
-                out=None, workspace=None):
-    """Single-call layer (hkmoe_moe_forward).  Returns the bf16 [T, H] output."""
+                out=None, workspace=None, packed=False):
+    """Single-call layer (hkmoe_moe_forward).  Returns the bf16 [T, H] output.
+    ``packed``: w13_q / w2_q come from :func:`pack_weights`."""
     _check_dev(x_q, logits, w13_q, w2_q)
     t, hidden = x_q.shape
     e, two_i, _ = w13_q.shape
@@ -77,12 +91,12 @@ def moe_forward(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k,
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=x_q.device)
     tk_kernel.dispatch_moe(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k, out,
-                           workspace)
+                           workspace, packed=packed)
     return out
 
 
 def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k,
-                      keep_h=False):
+                      keep_h=False, packed=False):
     """The layer one kernel at a time (the same kernels hkmoe_moe_forward
     enqueues); returns a dict of every intermediate.  With ``keep_h`` the block
     path also runs GEMM 1 once more with a bf16 output (``h``) for inspection."""
@@ -118,31 +132,39 @@ def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, to
     if block:
         tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
                                          r["offsets"], r["mtile_offsets"], r["hq"], r["hs"],
-                                         r["tile_ctr"][:8])
+                                         r["tile_ctr"][:8], packed=packed)
         if keep_h:  # static tile order for the inspection pass
             tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
-                                             r["offsets"], r["mtile_offsets"], r["h"], None)
+                                             r["offsets"], r["mtile_offsets"], r["h"], None,
+                                             packed=packed)
     else:
         tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
                                          r["offsets"], r["mtile_offsets"], r["h"], r["amax"],
-                                         r["tile_ctr"][:8])
+                                         r["tile_ctr"][:8], packed=packed)
         tk_kernel.dispatch_requant(r["h"], r["amax"], r["hq"], r["hs"])
     tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2_q, w2_scale, r["offsets"],
-                                     r["mtile_offsets"], r["y"], r["tile_ctr"][8:])
+                                     r["mtile_offsets"], r["y"], r["tile_ctr"][8:],
+                                     packed=packed)
     tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])
     return r
 
 
 class MoELayer:
     """FP8 MoE FFN layer: e4m3 expert weights with per-tensor ([E]) or
-    128x128 block scales; runs hkmoe_moe_forward with a cached workspace."""
+    128x128 block scales; runs hkmoe_moe_forward with a cached workspace.
+    With ``pack`` (default) the weights are repacked once, here, into the
+    grouped GEMMs' tile layout; the layer then holds only the packed copies."""
 
-    def __init__(self, w13_q, w13_scale, w2_q, w2_scale, top_k):
+    def __init__(self, w13_q, w13_scale, w2_q, w2_scale, top_k, pack=True):
         _check_dev(w13_q, w2_q)
         if w13_q.dtype != F8 or w2_q.dtype != F8:
             raise RuntimeError("MoELayer: weights must be float8_e4m3fn")
-        self.w13_q, self.w13_scale = w13_q.contiguous(), w13_scale.contiguous()
-        self.w2_q, self.w2_scale = w2_q.contiguous(), w2_scale.contiguous()
+        self.packed = bool(pack)
+        if self.packed:
+            self.w13_q, self.w2_q = pack_weights(w13_q, gate_up=True), pack_weights(w2_q)
+        else:
+            self.w13_q, self.w2_q = w13_q.contiguous(), w2_q.contiguous()
+        self.w13_scale, self.w2_scale = w13_scale.contiguous(), w2_scale.contiguous()
         self.top_k = int(top_k)
         self.num_experts, two_i, self.hidden = w13_q.shape
         self.inter = two_i // 2
@@ -160,4 +182,4 @@ class MoELayer:
     def __call__(self, x_q, x_scale, logits, out=None):
         ws = self.workspace(x_q.shape[0], x_q.device)
         return moe_forward(x_q, x_scale, logits, self.w13_q, self.w13_scale, self.w2_q,
-                           self.w2_scale, self.top_k, out=out, workspace=ws)
+                           self.w2_scale, self.top_k, out=out, workspace=ws, packed=self.packed)

@@ -45,6 +45,12 @@ enum hkmoe_scale_mode {
   HKMOE_SCALE_BLOCK = 1   /* activations 1x128 groups, weights 128x128 blocks */
 };
 
+/* Byte layout of expert weights [E, N, K] given to the grouped GEMMs. */
+enum hkmoe_weight_layout {
+  HKMOE_W_ROWS = 0,  /* row-major [E, N, K] */
+  HKMOE_W_PACKED = 1 /* hkmoe_pack_weights output (same size) */
+};
+
 /* Library version (major*10000 + minor*100 + patch) and last error text. */
 int hkmoe_version(void);
 const char* hkmoe_last_error(void);
@@ -121,6 +127,8 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
  *           out_format HKMOE_BF16: h bf16 [rows, I] (h_aux unused), or
  *           out_format HKMOE_E4M3: the 1x128-group requantisation of that bf16 h
  *           is fused in: h e4m3 [rows, I], h_aux = group scales [I/128, rows].
+ *   w_layout: HKMOE_W_ROWS, or HKMOE_W_PACKED for w13 packed by
+ *   hkmoe_pack_weights(..., gate_up = I) (same results, bit for bit).
  *   tile_counters: NULL (static tile order) or 8 zeroed ints, consumed by the
  *   call (per-XCD tile queues keep ragged tiles L2-local; zero before reuse).
  *   Requires H % 128 == 0, I % 128 == 0, H <= 16384.
@@ -129,8 +137,9 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
                         int32_t gather_div, int64_t x_rows, const void* w13,
                         const float* w13_scale, const int32_t* offsets,
                         const int32_t* mtile_offsets, int64_t rows, int32_t num_experts,
-                        int32_t hidden, int32_t inter, int scale_mode, int out_format, void* h,
-                        float* h_aux, int32_t* tile_counters, hkmoe_stream_t stream);
+                        int32_t hidden, int32_t inter, int scale_mode, int w_layout,
+                        int out_format, void* h, float* h_aux, int32_t* tile_counters,
+                        hkmoe_stream_t stream);
 
 /*
  * Requantise a bf16 intermediate to e4m3 for GEMM 2.
@@ -144,13 +153,27 @@ int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, co
 /*
  * Grouped GEMM 2:  y[p] = bf16( deq(hq[p]) . deq(W2[e])^T ),  w2 [E, H, I].
  *   TENSOR: hs [1], w2_scale [E];  BLOCK: hs_t [I/128, R], w2_scale [E, H/128, I/128].
+ *   w_layout: HKMOE_W_ROWS, or HKMOE_W_PACKED (hkmoe_pack_weights, gate_up = 0).
  *   tile_counters: as for hkmoe_grouped_gemm1.
  *   Requires H % 256 == 0, I % 128 == 0.
  */
 int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
                         const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
                         int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
-                        void* y, int32_t* tile_counters, hkmoe_stream_t stream);
+                        int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream);
+
+/*
+ * Load-time weight packing for the grouped GEMMs: w [E, N, K] e4m3 row-major
+ * -> packed (E*N*K bytes, another buffer).  Every 256-row N tile x 128-byte
+ * K step becomes one contiguous 32 KiB block in the GEMM's LDS stage order,
+ * so a tile's weights stream sequentially.  gate_up = I for the fused gate/up
+ * weights of GEMM 1 (N = 2I: rows [gate | up]), 0 otherwise.
+ * Requires N % 256 == 0, K % 128 == 0 (gate_up: N == 2*gate_up).
+ * No reference counterpart (the reference's GEMMs read [N, K] rows directly);
+ * it plays the role of a checkpoint-load weight shuffle.
+ */
+int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k, int32_t gate_up,
+                       void* packed, hkmoe_stream_t stream);
 
 /*
  * Top-k weighted unpermute/combine:
@@ -163,17 +186,16 @@ int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, i
 /*
  * Whole layer: route -> scatter -> GEMM1+SiLU*up -> requant -> GEMM2 -> combine.
  *   x_q [T,H] e4m3; x_scale [1] (TENSOR) or [T, H/128] (BLOCK);
- *   logits [T,E] fp32; w13/w2 and scales as above; out [T,H] bf16.
- *   workspace: device buffer of hkmoe_moe_workspace_size(...) bytes, 256-byte
- *   aligned.  Optional outputs (may be NULL): topk_idx [T,k] int32,
- *   topk_w [T,k] fp32 are written into the workspace otherwise.
+ *   logits [T,E] fp32; w13/w2 and scales as above, both in w_layout; out [T,H]
+ *   bf16.  workspace: device buffer of hkmoe_moe_workspace_size(...) bytes,
+ *   256-byte aligned, holding every intermediate (routing, permutation, h, y).
  */
 size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k,
                                 int32_t hidden, int32_t inter, int scale_mode);
 int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
                       const float* w13_scale, const void* w2, const float* w2_scale,
                       int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
-                      int32_t inter, int scale_mode, void* out, void* workspace,
+                      int32_t inter, int scale_mode, int w_layout, void* out, void* workspace,
                       size_t workspace_bytes, hkmoe_stream_t stream);
 
 /*

@@ -71,13 +71,18 @@ def test_routing_argument_errors(lib):
 def test_moe_forward_argument_errors(lib):
     fake = ctypes.c_void_p(0x1000)
     i64, i32 = ctypes.c_int64, ctypes.c_int32
-    args = [fake] * 7 + [i64(64), i32(8), i32(2), i32(4096), i32(1024), 0, fake, None, ctypes.c_size_t(0), None]
+    args = [fake] * 7 + [i64(64), i32(8), i32(2), i32(4096), i32(1024), 0, 0, fake, None, ctypes.c_size_t(0),
+                         None]
     assert lib.hkmoe_moe_forward(*args) == 4  # HKMOE_ERR_WORKSPACE
     assert "workspace" in _err(lib)
     args[12] = 2  # bad scale mode
     assert lib.hkmoe_moe_forward(*args) == 1
     assert "scale_mode" in _err(lib)
     args[12] = 0
+    args[13] = 3  # bad weight layout
+    assert lib.hkmoe_moe_forward(*args) == 1
+    assert "w_layout" in _err(lib)
+    args[13] = 0
     args[10] = i32(4000)  # hidden not a multiple of 256
     assert lib.hkmoe_moe_forward(*args) == 1
     assert "hidden=4000" in _err(lib)
@@ -88,11 +93,31 @@ def test_grouped_gemm_format_errors(lib):
     i64, i32 = ctypes.c_int64, ctypes.c_int32
     # e4m3 intermediate output is only defined for block scales
     rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, i64(128),
-                                 i32(8), i32(256), i32(128), 0, 2, fake, fake, None, None)
+                                 i32(8), i32(256), i32(128), 0, 0, 2, fake, fake, None, None)
     assert rc == 1 and "out_format" in _err(lib)
     rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, i64(128),
-                                 i32(8), i32(256), i32(96), 1, 0, fake, fake, None, None)
+                                 i32(8), i32(256), i32(96), 1, 0, 0, fake, fake, None, None)
     assert rc == 1 and "inter=96" in _err(lib)
+    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, i64(128),
+                                 i32(8), i32(256), i32(128), 1, 5, 0, fake, fake, None, None)
+    assert rc == 1 and "w_layout" in _err(lib)
+    rc = lib.hkmoe_grouped_gemm2(fake, fake, fake, fake, fake, fake, i64(128), i32(8), i32(256), i32(128),
+                                 1, 2, fake, None, None)
+    assert rc == 1 and "w_layout" in _err(lib)
+
+
+def test_pack_weights_argument_errors(lib):
+    fake, other = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000)
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    assert lib.hkmoe_pack_weights(fake, i64(4), i64(384), i64(256), i32(0), other, None) == 1
+    assert "N=384" in _err(lib)
+    assert lib.hkmoe_pack_weights(fake, i64(4), i64(512), i64(192), i32(0), other, None) == 1
+    assert lib.hkmoe_pack_weights(fake, i64(4), i64(512), i64(256), i32(128), other, None) == 1
+    assert "gate_up=128" in _err(lib)
+    assert lib.hkmoe_pack_weights(fake, i64(4), i64(512), i64(256), i32(0), fake, None) == 1
+    assert "in-place" in _err(lib)
+    # nothing to do for zero experts: succeeds without touching the GPU
+    assert lib.hkmoe_pack_weights(fake, i64(0), i64(512), i64(256), i32(256), other, None) == 0
 
 
 def _align(x):

@@ -119,6 +119,33 @@ def test_moe_single_call_matches_steps(hk, name):
     assert torch.equal(o1.view(torch.int16), out.view(torch.int16))
 
 
+@pytest.mark.parametrize("name", ["tensor_e8k2", "block_e16k4_skew", "block_e64k8_skew", "tensor_e5k5"])
+def test_packed_weights_bit_exact(hk, name):
+    """Grouped GEMMs on hkmoe_pack_weights output == on row-major weights, bit
+    for bit, in every intermediate (the pack is a pure relayout)."""
+    d = synth.make_moe(seed=13, **SMALL[name])
+    g = moe_inputs_to_gpu(d)
+    w13p = hk.pack_weights(g["w13_q"], gate_up=True)
+    w2p = hk.pack_weights(g["w2_q"])
+    torch.cuda.synchronize()
+    # a relayout: the same multiset of bytes, and not the identity
+    for w, p in ((g["w13_q"], w13p), (g["w2_q"], w2p)):
+        wb, pb = w.view(torch.uint8).flatten(), p.view(torch.uint8).flatten()
+        assert torch.equal(torch.sort(wb).values, torch.sort(pb).values)
+        assert not torch.equal(wb, pb)
+    ref = _run_steps(hk, g, keep_h=True)
+    r = hk.moe_forward_steps(g["x_q"], g["x_scale"], g["logits"], w13p, g["w13_scale"], w2p,
+                             g["w2_scale"], g["top_k"], keep_h=True, packed=True)
+    torch.cuda.synchronize()
+    for key in ("h", "hq", "hs", "y", "out"):
+        a, b = ref[key], r[key]
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), key
+    out = hk.moe_forward(g["x_q"], g["x_scale"], g["logits"], w13p, g["w13_scale"], w2p,
+                         g["w2_scale"], g["top_k"], packed=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref["out"].view(torch.int16))
+
+
 def test_routing_ties_and_edges(hk):
     """Ties resolve to the lower expert id; T not a multiple of the block; E not a power of 2."""
     rng = np.random.default_rng(3)
