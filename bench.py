@@ -53,6 +53,9 @@ def parse():
                     help="expert weight layout: packed once at layer construction (default) or row-major")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (counter calibration)")
+    ap.add_argument("--summarize-profile", metavar="DIR", default=None,
+                    help="no GPU work: turn the rocprofv3 output under DIR (trace/, FETCH_SIZE/, "
+                         "WRITE_SIZE/) of this config into profiles/*.md and profiles/traffic.json")
     return ap.parse_args()
 
 
@@ -195,8 +198,139 @@ def cpu_baseline(inp, cfg, budget_s):
                       f"{elapsed:.1f} s"}
 
 
+# ----------------------------------------------------------------------------
+# rocprofv3 summaries (host only)
+# ----------------------------------------------------------------------------
+PROF_TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d {d}/trace -o run -- "
+                  "python3 bench.py --config {c} --steps 5 --warmup 2 --no-cpu > {d}/bench.json")
+PROF_PMC_CMD = ("rocprofv3 --pmc {ctr} --output-format csv -d {d}/{ctr} -o run -- "
+                "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu --calibrate-copy")
+CALIB_BYTES = 1 << 30
+
+
+def _kernel_label(name):
+    """Short label of a kernel of this library (None for other kernels)."""
+    if "gemm_fp8_persistent" in name:
+        epi = name.split("Epi)")[1][0] if "Epi)" in name else "?"
+        return "grouped_gemm1" if epi in "23" else "grouped_gemm2"
+    if name.startswith("hkmoe::"):
+        return name[len("hkmoe::"):].split("(")[0].replace("_kernel", "")
+    return None
+
+
+def _algorithmic_bytes(cfg, active):
+    """Compulsory HBM bytes per launch (inputs read once, outputs written once;
+    weights of the `active` experts only)."""
+    T, H, I, k = cfg["T"], cfg["H"], cfg["I"], cfg["k"]
+    rows = T * k
+    sc_x = rows * (H // 128) * 4 if cfg["block"] else 4
+    sc_h = rows * (I // 128) * 4 if cfg["block"] else 4
+    g1 = active * 2 * I * H + T * H + sc_x + rows * I + sc_h
+    g2 = active * H * I + rows * I + sc_h + rows * H * 2
+    comb = rows * H * 2 + T * H * 2 + rows * 8
+    return {"grouped_gemm1": g1, "grouped_gemm2": g2, "combine": comb}
+
+
+def summarize_profile(args):
+    import csv
+    import collections
+    cfg = CONFIGS[args.config]
+    d = args.summarize_profile
+    out_dir = os.path.join(ROOT, "profiles")
+    os.makedirs(out_dir, exist_ok=True)
+    stats = os.path.join(d, "trace", "run_kernel_stats.csv")
+    rows = []
+    with open(stats) as f:
+        for r in csv.DictReader(f):
+            lab = _kernel_label(r["Name"])
+            if lab is None:
+                continue
+            rows.append((lab, int(r["Calls"]), float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3,
+                         float(r["MaxNs"]) / 1e3, float(r["TotalDurationNs"]) / 1e6))
+    tot = sum(r[5] for r in rows)
+    name = f"moe_layer_{args.config}"
+    with open(os.path.join(out_dir, f"{name}_kernels.md"), "w") as f:
+        f.write(f"# rocprofv3 kernel trace: MoE layer, workload `{args.config}`\n\n")
+        f.write(f"Config: {json.dumps(cfg)}\n\n")
+        with open(os.path.join(d, "bench.json")) as bj:
+            b = json.loads([ln for ln in bj if ln.startswith("{")][-1])
+        f.write(f"bench line of the traced run: value {b['value']} {b['unit']}, "
+                f"{b['ms_per_step']} ms/step, weights {b['config'].get('weights')}, "
+                f"active experts {b['config']['active_experts']}, event-timed kernels (ms): "
+                f"{json.dumps(b['kernels_ms'])}\n\n")
+        f.write("Command (repo root; bench.py runs warmup + timed steps + a 10-iteration "
+                "per-kernel pass, so call counts include all of them):\n\n")
+        f.write("    " + PROF_TRACE_CMD.format(d="<out>", c=args.config) + "\n\n")
+        f.write("| kernel | calls | avg us | min us | max us | share of library time |\n|---|---|---|---|---|---|\n")
+        for lab, n, avg, mn, mx, t in sorted(rows, key=lambda r: -r[5]):
+            f.write(f"| {lab} | {n} | {avg:.1f} | {mn:.1f} | {mx:.1f} | {100 * t / tot:.1f}% |\n")
+    # traffic passes
+    per = {}
+    calib = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        path = os.path.join(d, ctr, "run_counter_collection.csv")
+        agg = collections.defaultdict(lambda: collections.defaultdict(float))
+        copies = collections.defaultdict(float)
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] != ctr:
+                    continue
+                if r["Kernel_Name"] == "__amd_rocclr_copyBuffer":
+                    copies[r["Dispatch_Id"]] += float(r["Counter_Value"])
+                lab = _kernel_label(r["Kernel_Name"])
+                if lab is not None:
+                    agg[lab][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        big = max(copies.values())  # the 1 GiB calibration copy is the largest copy
+        calib[ctr] = (big, CALIB_BYTES / (big * 1024.0))
+        for lab, disp in agg.items():
+            per.setdefault(lab, {})[ctr] = sum(disp.values()) / len(disp)
+    with open(os.path.join(d, "bench.json")) as f:
+        line = [ln for ln in f if ln.startswith("{")][-1]
+    bench = json.loads(line)
+    active = bench["config"]["active_experts"]
+    algo = _algorithmic_bytes(cfg, active)
+    traffic = {}
+    with open(os.path.join(out_dir, f"{name}_traffic.md"), "w") as f:
+        f.write(f"# HBM traffic per launch: MoE layer, workload `{args.config}`\n\n")
+        f.write("Two counter passes, one counter each (repo root):\n\n")
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            f.write("    " + PROF_PMC_CMD.format(d="<out>", ctr=ctr, c=args.config) + "\n")
+        f.write("\nCalibration: `--calibrate-copy` runs one 1 GiB device-to-device copy "
+                "(`__amd_rocclr_copyBuffer`, reads and writes 1 GiB).  Factor = 1 GiB / counter "
+                "reading of that copy:\n\n")
+        for ctr, (raw, fac) in calib.items():
+            f.write(f"- {ctr}: {raw:,.0f} KiB for the 1 GiB copy -> factor {fac:.3f}\n")
+        f.write("\n| kernel | FETCH KiB (raw) | WRITE KiB (raw) | HBM read GB | HBM write GB | "
+                "algorithmic GB | measured / algorithmic |\n|---|---|---|---|---|---|---|\n")
+        for lab in sorted(per, key=lambda x: -per[x].get("FETCH_SIZE", 0)):
+            fe = per[lab].get("FETCH_SIZE", 0.0)
+            wr = per[lab].get("WRITE_SIZE", 0.0)
+            rd_b = fe * 1024 * calib["FETCH_SIZE"][1]
+            wr_b = wr * 1024 * calib["WRITE_SIZE"][1]
+            traffic[f"{args.config}:{lab}"] = round(rd_b + wr_b)
+            a = algo.get(lab)
+            f.write(f"| {lab} | {fe:,.0f} | {wr:,.0f} | {rd_b / 1e9:.3f} | {wr_b / 1e9:.3f} | "
+                    + (f"{a / 1e9:.3f} | {(rd_b + wr_b) / a:.2f} |\n" if a else "- | - |\n"))
+        f.write(f"\nAlgorithmic bytes: operands read once, outputs written once, weights of the "
+                f"{active} active experts only (activations e4m3, intermediates e4m3 + fp32 group "
+                f"scales, y and out bf16).\n")
+    tj = os.path.join(out_dir, "traffic.json")
+    old = {}
+    if os.path.exists(tj):
+        with open(tj) as f:
+            old = json.load(f)
+    old.update(traffic)
+    with open(tj, "w") as f:
+        json.dump(old, f, indent=1, sort_keys=True)
+    print(json.dumps({"written": [f"{name}_kernels.md", f"{name}_traffic.md", "traffic.json"],
+                      "traffic": traffic}))
+
+
 def main():
     args = parse()
+    if args.summarize_profile:
+        summarize_profile(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: run with --gpus 1 "
                                    "(multi-GPU sharding is a design note, not a measured path)"}))
