@@ -11,13 +11,17 @@
 //  * two LDS stages of 64 KiB (+1 KiB of activation scales) filled by
 //    buffer_load_dwordx4 ... lds (no VGPR staging): 128-byte row segments, i.e.
 //    whole L2 lines per lane octet.
-//  * ping-pong: waves 4-7 (rows 128-255) run half a K step behind waves 0-3
-//    (rows 0-127).  Every wave passes two barriers per K step and each group
-//    one extra barrier at opposite ends of the K loop, so on every SIMD one
-//    wave issues MFMAs while the other reads its fragments from LDS.  Each
-//    group DMAs its own half of A; group 0 also DMAs B one step ahead; every
-//    wave waits for its own DMA (vmcnt) and LDS reads (lgkmcnt) before a
-//    barrier, which is what makes a stage visible / free for the others.
+//  * ping-pong: each K step is four barrier-separated phases per wave:
+//    memory (LDS fragment reads + DMA issue), compute (MFMAs from registers
+//    only, raised wave priority), memory, compute.  Waves 4-7 (rows 128-255)
+//    run one phase behind waves 0-3, and each group passes one extra barrier
+//    at opposite ends of the K loop, so on every SIMD one wave issues MFMAs
+//    while the other reads LDS and issues loads.  Each group DMAs its own A
+//    half one step ahead and half of B two steps ahead (a stage's B half is
+//    free once both groups have read their B fragments, two phases before
+//    its A half); every wave waits for its own DMA (vmcnt) and LDS reads
+//    (lgkmcnt) before a barrier, which is what makes a stage visible / free
+//    for the others.
 //  * 16-byte chunk c of LDS row r is stored at c ^ ((r & 7) ^ ((r >> 3) & 1)):
 //    the ds_read_b128 operand reads of 16 consecutive rows are bank-conflict
 //    free whether the LDS serves 8 or 16 lanes per cycle, and the XOR is a lane
@@ -275,36 +279,39 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       as_voff = static_cast<int>(ar * p.as_rs) * 4;
     }
 
-    // DMA instructions of one K step, in a fixed order: the own A half (4),
-    // B (8, group 0 only), the activation scales (1, waves 0-1 of each group).
-    // They are issued a few at a time between the MFMAs of the first half-step
-    // so that texture-queue stalls overlap queued MFMA work.
-    constexpr int kOpsPerSub = 4;
-    auto issue_op = [&](int kt, int q) {
+    // DMA instructions of one K step issued by this wave.  issue_a: its
+    // group's A half (4, dead 16-row sub-tiles skipped) and, for waves 0-1 of
+    // each group, the activation scales (1).  issue_b: exactly 4 loads, half
+    // of the B stage (group 0 rows 0-127, group 1 rows 128-255); being the
+    // last 4 loads a wave issues, they are what vmcnt(4) leaves in flight.
+    auto issue_a = [&](int kt) {
       uint8_t* sa = smem + (kt & 1) * kStageBytes;
-      uint8_t* sb = sa + kTileBytes;
       const int koff = kt * kBK;
-      if (q < 4) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
         const int r8 = wave_row0 + 32 * q + 8 * wg;  // first row of this wave load
         if ((r8 & ~15) < valid) load_lds_16B(a_srd, sa + r8 * kBK, a_voff[q], koff);
-      } else if (q < 12) {
-        if (grp == 0) {
-          const int i = q - 4;
-          const int boff = kSilu ? (32 * (i >> 1) + ((i & 1) ? p.n_out : 0)) : 32 * i;
-          const int ioff = p.b_packed ? 32 * i * kBK : boff * p.K;
-          load_lds_16B(b_srd, sb + (32 * i + 8 * wg) * kBK, b_voff, kt * b_kstride + ioff);
-        }
-      } else if (q == 12) {
-        if (scale_loader) {
-          const i32x4 as_srd = make_srd(p.a_scale, 0xffffffffu);
-          load_lds_4B(as_srd, sb + kTileBytes + (wave_row0 + wg * 64) * 4, as_voff,
-                      static_cast<int>(kt * p.as_ks) * 4);
-        }
+      }
+      if (scale_loader) {
+        const i32x4 as_srd = make_srd(p.a_scale, 0xffffffffu);
+        load_lds_4B(as_srd, sa + 2 * kTileBytes + (wave_row0 + wg * 64) * 4, as_voff,
+                    static_cast<int>(kt * p.as_ks) * 4);
       }
     };
-    auto issue_step = [&](int kt) {
+    auto issue_b = [&](int kt) {
+      uint8_t* sb = smem + (kt & 1) * kStageBytes + kTileBytes;
 #pragma unroll
-      for (int q = 0; q < 13; ++q) issue_op(kt, q);
+      for (int q = 0; q < 4; ++q) {
+        const int i = grp * 4 + q;
+        const int boff = kSilu ? (32 * (i >> 1) + ((i & 1) ? p.n_out : 0)) : 32 * i;
+        const int ioff = p.b_packed ? 32 * i * kBK : boff * p.K;
+        load_lds_16B(b_srd, sb + (32 * i + 8 * wg) * kBK, b_voff, kt * b_kstride + ioff);
+      }
+    };
+    // every load of this wave except its last issue_b has completed
+    auto wait_dma = [&](bool b_in_flight) {
+      if (b_in_flight) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
 
     f32x4 acc[8][4];
@@ -326,8 +333,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         bs_lds[t] = bs[(h ? nb1 : nb0) * k_steps + (t - h * k_steps)];
       }
     }
-    issue_step(0);
-    if (grp == 1) sync_lds();  // group 1 runs one barrier (half a step) behind
+    issue_a(0);
+    issue_b(0);
+    if (k_steps > 1) issue_b(1);
+    wait_dma(k_steps > 1);     // stage 0 (and the weight scales) visible to all
+    if (grp == 1) sync_lds();  // group 1 runs one phase behind group 0
 
     // block scales: the accumulator holds sum / (sa_prev[i] * sb_prev[h])
     float sa_prev[8];
@@ -335,17 +345,30 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     for (int i = 0; i < 8; ++i) sa_prev[i] = 1.0f;
     float sb_prev0 = 1.0f, sb_prev1 = 1.0f;
 
+    // Four barrier-separated phases per K step: memory (LDS fragment reads,
+    // DMA issue), compute (MFMAs from registers only), memory, compute.  Group
+    // 1 is one phase behind, so on every SIMD one wave issues MFMAs while the
+    // other reads LDS.  Phase p of the block is group 0's phase p and group
+    // 1's phase p-1.  Stage kt is read in phases 4kt..4kt+3, its B fragments
+    // only in 4kt and 4kt+1: so A(kt+1) is issued in the first memory phase
+    // of step kt (phases 4kt / 4kt+1) and B(kt+2), into the B half of stage
+    // kt, in the second (phases 4kt+2 / 4kt+3), more than a step ahead.
+    // Stage kt+1 is first read in phase 4kt+4: every wave waits for all its
+    // loads but the newest B(kt+2) before the barrier ending phase 4kt+3
+    // (group 0: end of its second compute phase; group 1: end of its second
+    // memory phase).
     for (int kt = 0; kt < k_steps; ++kt) {
-      sync_stage();  // own DMA of step kt done (group 0: also B) -> stage kt visible
       const bool more = kt + 1 < k_steps;
-
       const uint8_t* sa = smem + (kt & 1) * kStageBytes;
       const uint8_t* sb = sa + kTileBytes;
 
-      i32x8 bf[4];
+      // ---- memory phase 1: B fragments, A sub-tiles 0-3, scales, DMA kt+1
+      i32x8 bf[4], af[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) bf[j] = read_frag(sb, wg * 64 + j * 16 + l16, lg, fx);
-
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i < live_sub) af[i] = read_frag(sa, wave_row0 + i * 16 + l16, lg, fx);
       float r0[8], r1[8];
       if constexpr (kBlockSc) {
         const float* sc = reinterpret_cast<const float*>(sb + kTileBytes) + wave_row0 + l16 * 8;
@@ -371,28 +394,47 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         sb_prev0 = sb_cur0;
         sb_prev1 = sb_cur1;
       }
+      if (more) issue_a(kt + 1);
+      sync_lds();
+      __builtin_amdgcn_sched_barrier(0);
 
-      i32x8 anext = read_frag(sa, wave_row0 + l16, lg, fx);
+      // ---- compute phase 1: sub-tiles 0-3
+      auto compute = [&](int i0) {
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i == 4) sync_lds();  // mid-step barrier: the other group switches phase
-        if (i < live_sub) {
-          const i32x8 af = anext;
-          if (i + 1 < live_sub) anext = read_frag(sa, wave_row0 + (i + 1) * 16 + l16, lg, fx);
-          if constexpr (kBlockSc) {
-            if (kt > 0) {
+        for (int i = i0; i < i0 + 4; ++i) {
+          if (i < live_sub) {
+            if constexpr (kBlockSc) {
+              if (kt > 0) {
 #pragma unroll
-              for (int j = 0; j < 4; ++j) acc[i][j] *= (kSilu && j >= 2) ? r1[i] : r0[i];
+                for (int j = 0; j < 4; ++j) acc[i][j] *= (kSilu && j >= 2) ? r1[i] : r0[i];
+              }
             }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = mfma_e4m3_16x16x128(bf[j], af[i - i0], acc[i][j]);
           }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = mfma_e4m3_16x16x128(bf[j], af, acc[i][j]);
         }
-        if (more && i < 4) {
+        __builtin_amdgcn_s_setprio(0);
+      };
+      compute(0);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+
+      // ---- memory phase 2: A sub-tiles 4-7
 #pragma unroll
-          for (int q = i * kOpsPerSub; q < (i == 3 ? 13 : (i + 1) * kOpsPerSub); ++q) issue_op(kt + 1, q);
-        }
-      }
+      for (int i = 0; i < 4; ++i)
+        if (i + 4 < live_sub) af[i] = read_frag(sa, wave_row0 + (i + 4) * 16 + l16, lg, fx);
+      const bool more2 = kt + 2 < k_steps;
+      if (more2) issue_b(kt + 2);
+      if (grp == 1) wait_dma(more2); else sync_lds();
+      __builtin_amdgcn_sched_barrier(0);
+
+      // ---- compute phase 2: sub-tiles 4-7
+      compute(4);
+      __builtin_amdgcn_sched_barrier(0);
+      if (grp == 0) wait_dma(more2); else __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (grp == 0) sync_lds();  // group 0's extra barrier pairs with group 1's first
 
