@@ -339,11 +339,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     wait_dma(k_steps > 1);     // stage 0 (and the weight scales) visible to all
     if (grp == 1) sync_lds();  // group 1 runs one phase behind group 0
 
-    // block scales: the accumulator holds sum / (sa_prev[i] * sb_prev[h])
+    // block scales: the accumulator holds sum / (sa_prev[i] * sb_prev[h]).
+    // The previous scales start at 0, so the first step's factor is exactly 0
+    // (the accumulators are 0 then): no first-step special case.
     float sa_prev[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sa_prev[i] = 1.0f;
-    float sb_prev0 = 1.0f, sb_prev1 = 1.0f;
+    for (int i = 0; i < 8; ++i) sa_prev[i] = 0.0f;
+    float sb_prev0 = 0.0f, sb_prev1 = 0.0f;
+    float sa_cur[8], sb_cur0 = 1.0f, sb_cur1 = 1.0f, rb0 = 0.0f, rb1 = 0.0f;
 
     // Four barrier-separated phases per K step: memory (LDS fragment reads,
     // DMA issue), compute (MFMAs from registers only), memory, compute.  Group
@@ -366,52 +369,58 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       i32x8 bf[4], af[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) bf[j] = read_frag(sb, wg * 64 + j * 16 + l16, lg, fx);
+      if (live_sub > 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (i < live_sub) af[i] = read_frag(sa, wave_row0 + i * 16 + l16, lg, fx);
-      float r0[8], r1[8];
+        for (int i = 0; i < 4; ++i) af[i] = read_frag(sa, wave_row0 + i * 16 + l16, lg, fx);
+      }
       if constexpr (kBlockSc) {
+        // this step's scales; the factors are formed in the compute phases
         const float* sc = reinterpret_cast<const float*>(sb + kTileBytes) + wave_row0 + l16 * 8;
         const f32x4 s_lo = *reinterpret_cast<const f32x4*>(sc);
         const f32x4 s_hi = *reinterpret_cast<const f32x4*>(sc + 4);
-        const float sa_cur[8] = {s_lo.x, s_lo.y, s_lo.z, s_lo.w, s_hi.x, s_hi.y, s_hi.z, s_hi.w};
-        float sb_cur0, sb_cur1;
+        sa_cur[0] = s_lo.x; sa_cur[1] = s_lo.y; sa_cur[2] = s_lo.z; sa_cur[3] = s_lo.w;
+        sa_cur[4] = s_hi.x; sa_cur[5] = s_hi.y; sa_cur[6] = s_hi.z; sa_cur[7] = s_hi.w;
         if constexpr (kSilu) {
           sb_cur0 = bs_lds[kt];
           sb_cur1 = bs_lds[k_steps + kt];
         } else {
           sb_cur0 = sb_cur1 = bs_lds[(wg >> 1) * k_steps + kt];
         }
-        const float rb0 = sb_prev0 * __builtin_amdgcn_rcpf(sb_cur0);
-        const float rb1 = sb_prev1 * __builtin_amdgcn_rcpf(sb_cur1);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float ra = sa_prev[i] * __builtin_amdgcn_rcpf(sa_cur[i]);
-          r0[i] = ra * rb0;
-          r1[i] = ra * rb1;
-          sa_prev[i] = sa_cur[i];
-        }
-        sb_prev0 = sb_cur0;
-        sb_prev1 = sb_cur1;
       }
       if (more) issue_a(kt + 1);
       sync_lds();
       __builtin_amdgcn_sched_barrier(0);
 
       // ---- compute phase 1: sub-tiles 0-3
+      // Block scales: factors r = (s_prev / s_cur) per sub-tile row and column
+      // half, applied to each accumulator right before its MFMA, so the
+      // multiplies of one accumulator overlap the MFMA of the previous one.
       auto compute = [&](int i0) {
         __builtin_amdgcn_s_setprio(1);
+        float r0[4], r1[4];
+        if constexpr (kBlockSc) {
+          if (i0 == 0) {
+            rb0 = sb_prev0 * __builtin_amdgcn_rcpf(sb_cur0);
+            rb1 = sb_prev1 * __builtin_amdgcn_rcpf(sb_cur1);
+            sb_prev0 = sb_cur0;
+            sb_prev1 = sb_cur1;
+          }
 #pragma unroll
-        for (int i = i0; i < i0 + 4; ++i) {
-          if (i < live_sub) {
-            if constexpr (kBlockSc) {
-              if (kt > 0) {
+          for (int u = 0; u < 4; ++u) {
+            const float ra = sa_prev[i0 + u] * __builtin_amdgcn_rcpf(sa_cur[i0 + u]);
+            r0[u] = ra * rb0;
+            r1[u] = ra * rb1;
+            sa_prev[i0 + u] = sa_cur[i0 + u];
+          }
+        }
+        // Skipped only when all four sub-tiles are dead; a partly live phase
+        // also computes its dead sub-tiles (stale fragments, never stored).
+        if (live_sub > i0) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] *= (kSilu && j >= 2) ? r1[i] : r0[i];
-              }
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = mfma_e4m3_16x16x128(bf[j], af[i - i0], acc[i][j]);
+          for (int t = 0; t < 16; ++t) {
+            const int u = t >> 2, j = t & 3;
+            if constexpr (kBlockSc) acc[i0 + u][j] *= (kSilu && j >= 2) ? r1[u] : r0[u];
+            acc[i0 + u][j] = mfma_e4m3_16x16x128(bf[j], af[u], acc[i0 + u][j]);
           }
         }
         __builtin_amdgcn_s_setprio(0);
@@ -422,9 +431,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       __builtin_amdgcn_sched_barrier(0);
 
       // ---- memory phase 2: A sub-tiles 4-7
+      if (live_sub > 4) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (i + 4 < live_sub) af[i] = read_frag(sa, wave_row0 + (i + 4) * 16 + l16, lg, fx);
+        for (int i = 0; i < 4; ++i) af[i] = read_frag(sa, wave_row0 + (i + 4) * 16 + l16, lg, fx);
+      }
       const bool more2 = kt + 2 < k_steps;
       if (more2) issue_b(kt + 2);
       if (grp == 1) wait_dma(more2); else sync_lds();
