@@ -122,16 +122,16 @@ def kernel_breakdown(inp, layer, iters=10):
     k = inp["top_k"]
     calls = [
         ("route_topk", lambda: tk_kernel.dispatch_route_topk(inp["logits"], r["topk_idx"], r["topk_w"], r["block_counts"])),
-        ("expert_offsets", lambda: tk_kernel.dispatch_expert_offsets(r["block_counts"], T, r["counts"], r["offsets"], r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"])),
+        ("expert_offsets", lambda: tk_kernel.dispatch_expert_offsets(r["block_counts"], T, r["counts"], r["offsets"], r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"], r["mtile_list"])),
         ("scatter", lambda: tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"], r["inv_perm"], None, None, None, None)),
     ]
     if block:
-        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8], packed=pk)))
+        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8], packed=pk, mtile_list=r["mtile_list"])))
     else:
-        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["h"], r["amax"], r["tile_ctr"][:8], packed=pk)))
+        calls.append(("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["h"], r["amax"], r["tile_ctr"][:8], packed=pk, mtile_list=r["mtile_list"])))
         calls.append(("requant", lambda: tk_kernel.dispatch_requant(r["h"], r["amax"], r["hq"], r["hs"])))
     calls += [
-        ("grouped_gemm2", lambda: tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2, inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], r["tile_ctr"][8:], packed=pk)),
+        ("grouped_gemm2", lambda: tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2, inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], r["tile_ctr"][8:], packed=pk, mtile_list=r["mtile_list"])),
         ("combine", lambda: tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])),
     ]
     ev = {name: [] for name, _ in calls}

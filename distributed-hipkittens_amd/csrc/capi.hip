@@ -126,6 +126,7 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
   p.nb = static_cast<int32_t>(n);
   p.n_out = static_cast<int32_t>(n);
   p.n_tiles = static_cast<int32_t>(n / kBN);
+  p.blk_m_log2 = 2;  // 4 x 8 tile blocks
   auto s = static_cast<hipStream_t>(stream);
   return out_dtype == HKMOE_BF16 ? launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s)
                                  : launch_gemm<Epi::kStoreF32, Scale::kTensor>(p, s);
@@ -151,8 +152,8 @@ int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_expert
 
 int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
                          int32_t* counts, int32_t* offsets, int32_t* block_base,
-                         int32_t* mtile_offsets, float* amax_reset, int32_t* tile_counters,
-                         hkmoe_stream_t stream) {
+                         int32_t* mtile_offsets, int32_t* mtile_list, float* amax_reset,
+                         int32_t* tile_counters, hkmoe_stream_t stream) {
   HK_REQUIRE(counts && offsets && block_base && mtile_offsets, "expert_offsets: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "expert_offsets: E=%d outside [1, %d]",
              num_experts, kMaxExperts);
@@ -163,7 +164,7 @@ int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_
   const int parts = kScanThreads / e_stride;
   hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(kScanThreads), 0,
                      static_cast<hipStream_t>(stream), block_counts, nblk, num_experts, e_stride,
-                     parts, counts, offsets, block_base, mtile_offsets, kBM, amax_reset,
+                     parts, counts, offsets, block_base, mtile_offsets, mtile_list, kBM, amax_reset,
                      tile_counters);
   return check_launch("expert_offsets_kernel");
 }
@@ -200,7 +201,8 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
 
 int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gather,
                         int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
-                        const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
+                        const int32_t* offsets, const int32_t* mtile_offsets,
+                        const int32_t* mtile_list, int64_t rows,
                         int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
                         int w_layout, int out_format, void* h, float* h_aux,
                         int32_t* tile_counters, hkmoe_stream_t stream) {
@@ -244,6 +246,8 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
   p.n_out = inter;
   p.n_tiles = inter / 128;
   p.b_packed = w_layout == HKMOE_W_PACKED;
+  p.mtile_list = mtile_list;
+  p.blk_m_log2 = 1;  // 2 x 16 tile blocks
   p.tile_ctr = tile_counters;
   auto s = static_cast<hipStream_t>(stream);
   if (scale_mode == HKMOE_SCALE_TENSOR) {
@@ -280,7 +284,8 @@ int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, co
 }
 
 int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
-                        const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
+                        const int32_t* offsets, const int32_t* mtile_offsets,
+                        const int32_t* mtile_list, int64_t rows,
                         int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
                         int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream) {
   HK_REQUIRE(hq && hs && w2 && w2_scale && offsets && mtile_offsets && y, "grouped_gemm2: null pointer");
@@ -313,6 +318,8 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
   p.n_out = hidden;
   p.n_tiles = hidden / kBN;
   p.b_packed = w_layout == HKMOE_W_PACKED;
+  p.mtile_list = mtile_list;
+  p.blk_m_log2 = 1;  // 2 x 16 tile blocks
   p.tile_ctr = tile_counters;
   auto s = static_cast<hipStream_t>(stream);
   return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kStoreBf16, Scale::kBlock>(p, s)
@@ -363,6 +370,7 @@ struct MoeWorkspace {
   int32_t* counts;
   int32_t* offsets;
   int32_t* mtile_offsets;
+  int32_t* mtile_list;  // [M tiles][2], at most ceil(T*k/256) + E tiles
   float* amax;
   int32_t* tile_ctr;  // HKMOE_TILE_COUNTERS
   int32_t* perm;
@@ -392,6 +400,7 @@ MoeWorkspace carve(uint8_t* base, int64_t t, int32_t e, int32_t k, int32_t hidde
   w.counts = reinterpret_cast<int32_t*>(take(e * 4));
   w.offsets = reinterpret_cast<int32_t*>(take((e + 1) * 4));
   w.mtile_offsets = reinterpret_cast<int32_t*>(take((e + 1) * 4));
+  w.mtile_list = reinterpret_cast<int32_t*>(take(((r + kBM - 1) / kBM + e) * 8));
   w.amax = reinterpret_cast<float*>(take(4));
   w.tile_ctr = reinterpret_cast<int32_t*>(take(HKMOE_TILE_COUNTERS * 4));
   w.perm = reinterpret_cast<int32_t*>(take(r * 4));
@@ -443,23 +452,25 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
   HK_TRY(hkmoe_route_topk(logits, num_tokens, num_experts, top_k, w.topk_idx, w.topk_w,
                           w.block_counts, stream));
   HK_TRY(hkmoe_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets,
-                              w.block_base, w.mtile_offsets, w.amax, w.tile_ctr, stream));
+                              w.block_base, w.mtile_offsets, w.mtile_list, w.amax, w.tile_ctr,
+                              stream));
   HK_TRY(hkmoe_scatter(w.topk_idx, num_tokens, num_experts, top_k, w.offsets, w.block_base, w.perm,
                        w.inv_perm, nullptr, nullptr, hidden, scale_mode, nullptr, nullptr, stream));
   if (block) {
     // GEMM 1 reads token rows through perm and writes the requantised e4m3
     // intermediate and its 1x128 group scales directly.
     HK_TRY(hkmoe_grouped_gemm1(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
-                               w.mtile_offsets, rows, num_experts, hidden, inter, scale_mode,
-                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream));
+                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter,
+                               scale_mode, w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream));
   } else {
     HK_TRY(hkmoe_grouped_gemm1(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
-                               w.mtile_offsets, rows, num_experts, hidden, inter, scale_mode,
-                               w_layout, HKMOE_BF16, w.h, w.amax, w.tile_ctr, stream));
+                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter,
+                               scale_mode, w_layout, HKMOE_BF16, w.h, w.amax, w.tile_ctr, stream));
     HK_TRY(hkmoe_requant(w.h, rows, inter, scale_mode, w.amax, w.hq, w.hs, stream));
   }
-  HK_TRY(hkmoe_grouped_gemm2(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, rows, num_experts,
-                             hidden, inter, scale_mode, w_layout, w.y, w.tile_ctr + 8, stream));
+  HK_TRY(hkmoe_grouped_gemm2(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list,
+                             rows, num_experts, hidden, inter, scale_mode, w_layout, w.y,
+                             w.tile_ctr + 8, stream));
   HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
   return HKMOE_OK;
 }

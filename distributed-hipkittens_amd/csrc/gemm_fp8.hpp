@@ -39,7 +39,11 @@
 //    consecutive columns of one output row per 16-row sub-tile: one activation
 //    scale per lane per sub-tile and block.
 //  * persistent grid (one 512-thread workgroup per CU).  Tiles form blocks of
-//    8 M tiles x 4 N tiles.  With tile counters (grouped GEMMs) every XCD (one
+//    bm x bn = 32 tiles (dense 4 x 8, grouped 2 x 16: a grouped block mostly
+//    spans one or two experts, whose 16 N tiles then share the A rows).  The
+//    grouped GEMMs walk M tiles in the order of an optional device list (full
+//    tiles first, so blocks hold tiles of equal cost).  With tile counters
+//    (grouped GEMMs) every XCD (one
 //    L2; workgroups are dispatched round-robin, so blockIdx % 8) owns the
 //    blocks b = x, x+8, ... and its 32 workgroups pull tiles of those blocks in
 //    order from the XCD's atomic counter, so they keep working on the same
@@ -72,6 +76,7 @@ struct GemmParams {
   float* c_scale;              // kSiluQuant: group scales, transposed [n_out/128, rows]
   const int32_t* offsets;      // [E+1] row offsets; nullptr = dense (one segment of `rows`)
   const int32_t* mtile_offsets;// [E+1] M-tile offsets; nullptr = dense
+  const int32_t* mtile_list;   // optional [M tiles][2] = (expert, first row), in schedule order
   float* amax;                 // kSiluBf16: running max |h| (uint-ordered), may be null
   int32_t* tile_ctr;           // optional: 8 zeroed per-XCD tile counters (dynamic schedule)
   int64_t rows;                // output rows (dense: M)
@@ -85,6 +90,7 @@ struct GemmParams {
   int32_t n_out;               // output columns (N, or I)
   int32_t n_tiles;             // N tiles per M tile
   int32_t b_packed;            // 1: b is in the packed tile layout of pack_weights_kernel
+  int32_t blk_m_log2;          // tile blocks are 2^blk_m_log2 M tiles x 32 / 2^blk_m_log2 N tiles
 };
 
 constexpr int kBM = 256, kBN = 256, kBK = 128;
@@ -174,9 +180,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   const int ld_chunk = (lane & 7) ^ swz(ld_row);
   const i32x4 a_srd = make_srd(p.a, p.a_bytes);
 
-  // tile blocks: 8 M tiles x 4 N tiles
-  const int nbn = (p.n_tiles + 3) >> 2;
-  const int nblocks = ((total_mtiles + 7) >> 3) * nbn;
+  // tile blocks: bm M tiles x bn N tiles, bm * bn = 32
+  const int bm = 1 << p.blk_m_log2, bn = 32 >> p.blk_m_log2;
+  const int nbn = (p.n_tiles + bn - 1) / bn;
+  const int nblocks = ((total_mtiles + bm - 1) / bm) * nbn;
   int* s_tile = reinterpret_cast<int*>(smem + kLdsData);
   const int xcd = blockIdx.x & 7;
   int steal = 0;          // queues visited so far (thread 0 only)
@@ -194,7 +201,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
           const int j = nslots > 0 ? atomicAdd(&p.tile_ctr[q], 1) : nslots;
           if (j >= nslots) { ++steal; continue; }
           const int b = q + 8 * (j >> 5), sl = j & 31;
-          const int m = 8 * (b / nbn) + (sl & 7), n = 4 * (b % nbn) + (sl >> 3);
+          const int m = bm * (b / nbn) + (sl & (bm - 1)), n = bn * (b % nbn) + (sl >> p.blk_m_log2);
           if (m < total_mtiles && n < p.n_tiles) t = m * p.n_tiles + n;
         }
         *s_tile = t;
@@ -212,7 +219,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         static_j += g;
         const int b = j >> 5, sl = j & 31;
         if (b >= nblocks) break;
-        const int m = 8 * (b / nbn) + (sl & 7), n = 4 * (b % nbn) + (sl >> 3);
+        const int m = bm * (b / nbn) + (sl & (bm - 1)), n = bn * (b % nbn) + (sl >> p.blk_m_log2);
         if (m < total_mtiles && n < p.n_tiles) { mt_glob = m; nt = n; found = true; }
       }
       if (!found) break;
@@ -225,6 +232,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     if (dense) {
       row0 = mt_glob * kBM;
       valid = static_cast<int>(min<int64_t>(kBM, p.rows - row0));
+    } else if (p.mtile_list != nullptr) {
+      e = p.mtile_list[2 * mt_glob];
+      row0 = p.mtile_list[2 * mt_glob + 1];
+      valid = min(kBM, p.offsets[e + 1] - row0);
     } else {
       int lo = 0, hi = p.num_experts;  // largest e with mtile_offsets[e] <= mt_glob
       while (hi - lo > 1) {

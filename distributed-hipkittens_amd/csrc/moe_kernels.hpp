@@ -121,7 +121,8 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot) {
 __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
     const int32_t* __restrict__ block_counts, int nblk, int num_experts, int e_stride, int parts,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ block_base,
-    int32_t* __restrict__ mtile_offsets, int tile_m, float* amax_reset, int32_t* tile_counters) {
+    int32_t* __restrict__ mtile_offsets, int32_t* __restrict__ mtile_list, int tile_m,
+    float* amax_reset, int32_t* tile_counters) {
   __shared__ int part_sum[kScanThreads];
   __shared__ int wave_tot[kScanThreads / 64];
   const int tid = threadIdx.x;
@@ -174,6 +175,29 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
     if (e == num_experts - 1) {
       offsets[num_experts] = off + cnt;
       mtile_offsets[num_experts] = moff + mt;
+    }
+  }
+  if (mtile_list != nullptr) {
+    // M-tile list [(expert, first row)]: every expert's full tiles first (in
+    // expert order), then the partial tiles.  Tiles of equal cost then sit
+    // together in the grouped GEMMs' schedule, so the workgroups that share a
+    // tile block stay in step and reuse its operands in L2.
+    const int q_full = cnt / tile_m;
+    const int q_part = (cnt % tile_m) ? 1 : 0;
+    const int full_base = block_exclusive_scan(q_full, wave_tot);
+    const int part_base = block_exclusive_scan(q_part, wave_tot);
+    __shared__ int n_full;
+    if (part == 0 && e == num_experts - 1) n_full = full_base + q_full;
+    __syncthreads();
+    if (part == 0 && e < num_experts) {
+      for (int s = 0; s < q_full; ++s) {
+        mtile_list[2 * (full_base + s)] = e;
+        mtile_list[2 * (full_base + s) + 1] = off + s * tile_m;
+      }
+      if (q_part) {
+        mtile_list[2 * (n_full + part_base)] = e;
+        mtile_list[2 * (n_full + part_base) + 1] = off + q_full * tile_m;
+      }
     }
   }
   if (tid == 0 && amax_reset != nullptr) *amax_reset = 0.0f;

@@ -14,6 +14,7 @@
 // this module only depends on pybind11 and the C ABI.
 #include <pybind11/pybind11.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -140,13 +141,17 @@ void dispatch_route_topk(py::object logits, py::object idx, py::object w, py::ob
                          static_cast<float*>(ww.ptr), static_cast<int32_t*>(b.ptr), current_stream()));
 }
 
+// Upper bound of the M tiles of T tokens over E experts (top-k <= min(E, 32)).
+int64_t mtile_list_ints(int64_t rows, int64_t e) { return 2 * ((rows + 255) / 256 + e); }
+
 void dispatch_expert_offsets(py::object bc, int64_t num_tokens, py::object counts, py::object offsets,
                              py::object block_base, py::object mtile_offsets, py::object amax,
-                             py::object tile_counters) {
+                             py::object tile_counters, py::object mtile_list) {
   auto b = as_tensor(bc, "block_counts"), c = as_tensor(counts, "counts"),
        o = as_tensor(offsets, "offsets"), bb = as_tensor(block_base, "block_base"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), am = as_tensor_opt(amax, "amax"),
-       tc = as_tensor_opt(tile_counters, "tile_counters");
+       tc = as_tensor_opt(tile_counters, "tile_counters"), ml = as_tensor_opt(mtile_list, "mtile_list");
+  want_dtype(ml, "mtile_list", kI32);
   for (auto* t : {&b, &c, &o, &bb, &mo}) want_dtype(*t, "int tensor", kI32);
   want_dtype(am, "amax", kF32);
   want_dtype(tc, "tile_counters", kI32);
@@ -155,10 +160,13 @@ void dispatch_expert_offsets(py::object bc, int64_t num_tokens, py::object count
   if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
   if (b.numel() < static_cast<int64_t>(hkmoe_route_blocks(num_tokens)) * e || bb.numel() < b.numel())
     throw std::runtime_error("block_counts/block_base too small");
+  if (ml.ptr && ml.numel() < mtile_list_ints(num_tokens * std::min<int64_t>(e, 32), e))
+    throw std::runtime_error("mtile_list must hold 2 * (ceil(T * min(E, 32) / 256) + E) ints");
   check(hkmoe_expert_offsets(static_cast<const int32_t*>(b.ptr), num_tokens, static_cast<int32_t>(e),
                              static_cast<int32_t*>(c.ptr), static_cast<int32_t*>(o.ptr),
                              static_cast<int32_t*>(bb.ptr), static_cast<int32_t*>(mo.ptr),
-                             static_cast<float*>(am.ptr), static_cast<int32_t*>(tc.ptr), current_stream()));
+                             static_cast<int32_t*>(ml.ptr), static_cast<float*>(am.ptr),
+                             static_cast<int32_t*>(tc.ptr), current_stream()));
 }
 
 void dispatch_scatter(py::object idx, py::object offsets, py::object block_base, py::object perm,
@@ -199,12 +207,15 @@ void dispatch_scatter(py::object idx, py::object offsets, py::object block_base,
 
 void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gather, int32_t gather_div,
                             py::object w13, py::object w13s, py::object offsets, py::object mtile_offsets,
-                            py::object h, py::object h_aux, py::object tile_counters, bool packed) {
+                            py::object h, py::object h_aux, py::object tile_counters, bool packed,
+                            py::object mtile_list) {
   auto x = as_tensor(x_q, "x"), xs = as_tensor(x_scale, "x_scale"), gth = as_tensor_opt(gather, "gather"),
        w = as_tensor(w13, "w13"), ws = as_tensor(w13s, "w13_scale"), o = as_tensor(offsets, "offsets"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), hh = as_tensor(h, "h"),
-       aux = as_tensor_opt(h_aux, "h_aux"), tc = as_tensor_opt(tile_counters, "tile_counters");
+       aux = as_tensor_opt(h_aux, "h_aux"), tc = as_tensor_opt(tile_counters, "tile_counters"),
+       ml = as_tensor_opt(mtile_list, "mtile_list");
   want_dtype(tc, "tile_counters", kI32);
+  want_dtype(ml, "mtile_list", kI32);
   if (tc.ptr && tc.numel() < 8) throw std::runtime_error("tile_counters must hold 8 ints");
   want_dtype(x, "x", kF8);
   want_dtype(w, "w13", kF8);
@@ -220,6 +231,7 @@ void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gathe
   if (w.shape[2] != hidden || w.shape[1] % 2) throw std::runtime_error("w13 must be [E, 2I, H]");
   if (hh.shape[1] != inter) throw std::runtime_error("h must be [rows, I]");
   if (gth.ptr && gth.numel() != rows) throw std::runtime_error("gather must hold one index per row");
+  if (ml.ptr && ml.numel() < mtile_list_ints(rows, e)) throw std::runtime_error("mtile_list too small");
   if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
   int fmt;
   if (hh.dtype == kBf16) fmt = HKMOE_BF16;
@@ -234,7 +246,8 @@ void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gathe
     throw std::runtime_error("e4m3 output needs h_aux [I/128, rows] group scales");
   check(hkmoe_grouped_gemm1(x.ptr, static_cast<const float*>(xs.ptr), static_cast<const int32_t*>(gth.ptr),
                             gather_div, x_rows, w.ptr, static_cast<const float*>(ws.ptr),
-                            static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr), rows,
+                            static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr),
+                            static_cast<const int32_t*>(ml.ptr), rows,
                             static_cast<int32_t>(e), static_cast<int32_t>(hidden), static_cast<int32_t>(inter),
                             mode, packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, fmt, hh.ptr,
                             static_cast<float*>(aux.ptr), static_cast<int32_t*>(tc.ptr), current_stream()));
@@ -261,12 +274,13 @@ void dispatch_requant(py::object h, py::object amax, py::object hq, py::object h
 
 void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::object w2s,
                             py::object offsets, py::object mtile_offsets, py::object y,
-                            py::object tile_counters, bool packed) {
+                            py::object tile_counters, bool packed, py::object mtile_list) {
   auto q = as_tensor(hq, "hq"), s = as_tensor(hs, "hs"), w = as_tensor(w2, "w2"),
        ws = as_tensor(w2s, "w2_scale"), o = as_tensor(offsets, "offsets"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), yy = as_tensor(y, "y"),
-       tc = as_tensor_opt(tile_counters, "tile_counters");
+       tc = as_tensor_opt(tile_counters, "tile_counters"), ml = as_tensor_opt(mtile_list, "mtile_list");
   want_dtype(tc, "tile_counters", kI32);
+  want_dtype(ml, "mtile_list", kI32);
   if (tc.ptr && tc.numel() < 8) throw std::runtime_error("tile_counters must hold 8 ints");
   want_dtype(q, "hq", kF8);
   want_dtype(w, "w2", kF8);
@@ -279,6 +293,7 @@ void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::obj
   if (w.shape[2] != inter) throw std::runtime_error("w2 must be [E, H, I]");
   if (yy.numel() != rows * hidden) throw std::runtime_error("y must be [rows, H]");
   if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
+  if (ml.ptr && ml.numel() < mtile_list_ints(rows, e)) throw std::runtime_error("mtile_list too small");
   const int mode = scale_mode_of(s);
   if (mode == HKMOE_SCALE_TENSOR && ws.numel() != e) throw std::runtime_error("w2_scale must be [E]");
   if (mode == HKMOE_SCALE_BLOCK &&
@@ -286,7 +301,8 @@ void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::obj
     throw std::runtime_error("block scales: hs [I/128, rows], w2_scale [E, H/128, I/128]");
   check(hkmoe_grouped_gemm2(q.ptr, static_cast<const float*>(s.ptr), w.ptr,
                             static_cast<const float*>(ws.ptr), static_cast<const int32_t*>(o.ptr),
-                            static_cast<const int32_t*>(mo.ptr), rows, static_cast<int32_t>(e),
+                            static_cast<const int32_t*>(mo.ptr), static_cast<const int32_t*>(ml.ptr), rows,
+                            static_cast<int32_t>(e),
                             static_cast<int32_t>(hidden), static_cast<int32_t>(inter), mode,
                             packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, yy.ptr, static_cast<int32_t*>(tc.ptr),
                             current_stream()));
@@ -408,16 +424,17 @@ PYBIND11_MODULE(tk_kernel, m) {
   m.def("dispatch_route_topk", &dispatch_route_topk);
   m.def("dispatch_expert_offsets", &dispatch_expert_offsets, py::arg("block_counts"), py::arg("num_tokens"),
         py::arg("counts"), py::arg("offsets"), py::arg("block_base"), py::arg("mtile_offsets"),
-        py::arg("amax") = py::none(), py::arg("tile_counters") = py::none());
+        py::arg("amax") = py::none(), py::arg("tile_counters") = py::none(),
+        py::arg("mtile_list") = py::none());
   m.def("dispatch_scatter", &dispatch_scatter);
   m.def("dispatch_grouped_gemm1", &dispatch_grouped_gemm1, py::arg("x_q"), py::arg("x_scale"), py::arg("gather"),
         py::arg("gather_div"), py::arg("w13"), py::arg("w13_scale"), py::arg("offsets"),
         py::arg("mtile_offsets"), py::arg("h"), py::arg("h_aux") = py::none(),
-        py::arg("tile_counters") = py::none(), py::arg("packed") = false);
+        py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none());
   m.def("dispatch_requant", &dispatch_requant);
   m.def("dispatch_grouped_gemm2", &dispatch_grouped_gemm2, py::arg("hq"), py::arg("hs"), py::arg("w2"),
         py::arg("w2_scale"), py::arg("offsets"), py::arg("mtile_offsets"), py::arg("y"),
-        py::arg("tile_counters") = py::none(), py::arg("packed") = false);
+        py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none());
   m.def("dispatch_combine", &dispatch_combine);
   m.def("dispatch_moe", &dispatch_moe, py::arg("x_q"), py::arg("x_scale"), py::arg("logits"), py::arg("w13"),
         py::arg("w13_scale"), py::arg("w2"), py::arg("w2_scale"), py::arg("top_k"), py::arg("out"),
@@ -428,6 +445,7 @@ PYBIND11_MODULE(tk_kernel, m) {
   m.def("dispatch_quant_tensor", &dispatch_quant_tensor);
   m.def("moe_workspace_size", &moe_workspace_size);
   m.def("route_blocks", [](int64_t t) { return hkmoe_route_blocks(t); });
+  m.def("mtile_list_ints", &mtile_list_ints, "ints of an M-tile list for `rows` expert rows over E experts");
   m.def("version", []() { return hkmoe_version(); });
   m.attr("SCALE_TENSOR") = static_cast<int>(HKMOE_SCALE_TENSOR);
   m.attr("SCALE_BLOCK") = static_cast<int>(HKMOE_SCALE_BLOCK);

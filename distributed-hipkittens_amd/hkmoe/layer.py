@@ -115,6 +115,7 @@ def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, to
         block_counts=torch.empty((nblk, e), **i32), block_base=torch.empty((nblk, e), **i32),
         counts=torch.empty(e, **i32), offsets=torch.empty(e + 1, **i32),
         mtile_offsets=torch.empty(e + 1, **i32), amax=torch.empty(1, **f32),
+        mtile_list=torch.empty(tk_kernel.mtile_list_ints(t * min(e, 32), e), **i32),
         tile_ctr=torch.empty(16, **i32),
         perm=torch.empty(rows, **i32), inv_perm=torch.empty(rows, **i32),
         hq=torch.empty((rows, inter), dtype=F8, device=dev),
@@ -126,13 +127,14 @@ def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, to
         r["h"] = torch.empty((rows, inter), dtype=torch.bfloat16, device=dev)
     tk_kernel.dispatch_route_topk(logits, r["topk_idx"], r["topk_w"], r["block_counts"])
     tk_kernel.dispatch_expert_offsets(r["block_counts"], t, r["counts"], r["offsets"],
-                                      r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"])
+                                      r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"],
+                                      r["mtile_list"])
     tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"],
                                r["inv_perm"], None, None, None, None)
     if block:
         tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
                                          r["offsets"], r["mtile_offsets"], r["hq"], r["hs"],
-                                         r["tile_ctr"][:8], packed=packed)
+                                         r["tile_ctr"][:8], packed=packed, mtile_list=r["mtile_list"])
         if keep_h:  # static tile order for the inspection pass
             tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
                                              r["offsets"], r["mtile_offsets"], r["h"], None,
@@ -140,11 +142,11 @@ def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, to
     else:
         tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale,
                                          r["offsets"], r["mtile_offsets"], r["h"], r["amax"],
-                                         r["tile_ctr"][:8], packed=packed)
+                                         r["tile_ctr"][:8], packed=packed, mtile_list=r["mtile_list"])
         tk_kernel.dispatch_requant(r["h"], r["amax"], r["hq"], r["hs"])
     tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2_q, w2_scale, r["offsets"],
                                      r["mtile_offsets"], r["y"], r["tile_ctr"][8:],
-                                     packed=packed)
+                                     packed=packed, mtile_list=r["mtile_list"])
     tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])
     return r
 

@@ -92,12 +92,17 @@ int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_expert
  *   mtile_offsets [E+1] (prefix sum of ceil(counts/256): the grouped GEMM's
  *   M-tile list), and zeroes *amax_reset and the HKMOE_TILE_COUNTERS ints at
  *   tile_counters when they are non-NULL.
+ *   mtile_list (may be NULL): [ceil(T*k/256) + E][2] int32; receives one
+ *   (expert, first row) pair per M tile, every expert's full 256-row tiles
+ *   first (expert order), then the partial tiles.  Passed to the grouped
+ *   GEMMs it sets their tile order (tiles of equal cost run together, which
+ *   keeps L2 reuse up); NULL there means expert order.
  */
 #define HKMOE_TILE_COUNTERS 16 /* 8 per grouped GEMM: one tile queue per XCD */
 int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
                          int32_t* counts, int32_t* offsets, int32_t* block_base,
-                         int32_t* mtile_offsets, float* amax_reset, int32_t* tile_counters,
-                         hkmoe_stream_t stream);
+                         int32_t* mtile_offsets, int32_t* mtile_list, float* amax_reset,
+                         int32_t* tile_counters, hkmoe_stream_t stream);
 
 /*
  * Routing step 3: stable scatter into expert-contiguous order.
@@ -129,6 +134,7 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
  *           is fused in: h e4m3 [rows, I], h_aux = group scales [I/128, rows].
  *   w_layout: HKMOE_W_ROWS, or HKMOE_W_PACKED for w13 packed by
  *   hkmoe_pack_weights(..., gate_up = I) (same results, bit for bit).
+ *   mtile_list: NULL (expert order) or the list written by hkmoe_expert_offsets.
  *   tile_counters: NULL (static tile order) or 8 zeroed ints, consumed by the
  *   call (per-XCD tile queues keep ragged tiles L2-local; zero before reuse).
  *   Requires H % 128 == 0, I % 128 == 0, H <= 16384.
@@ -136,7 +142,8 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
 int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gather,
                         int32_t gather_div, int64_t x_rows, const void* w13,
                         const float* w13_scale, const int32_t* offsets,
-                        const int32_t* mtile_offsets, int64_t rows, int32_t num_experts,
+                        const int32_t* mtile_offsets, const int32_t* mtile_list,
+                        int64_t rows, int32_t num_experts,
                         int32_t hidden, int32_t inter, int scale_mode, int w_layout,
                         int out_format, void* h, float* h_aux, int32_t* tile_counters,
                         hkmoe_stream_t stream);
@@ -154,11 +161,12 @@ int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, co
  * Grouped GEMM 2:  y[p] = bf16( deq(hq[p]) . deq(W2[e])^T ),  w2 [E, H, I].
  *   TENSOR: hs [1], w2_scale [E];  BLOCK: hs_t [I/128, R], w2_scale [E, H/128, I/128].
  *   w_layout: HKMOE_W_ROWS, or HKMOE_W_PACKED (hkmoe_pack_weights, gate_up = 0).
- *   tile_counters: as for hkmoe_grouped_gemm1.
+ *   mtile_list, tile_counters: as for hkmoe_grouped_gemm1.
  *   Requires H % 256 == 0, I % 128 == 0.
  */
 int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
-                        const int32_t* offsets, const int32_t* mtile_offsets, int64_t rows,
+                        const int32_t* offsets, const int32_t* mtile_offsets,
+                        const int32_t* mtile_list, int64_t rows,
                         int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
                         int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream);
 

@@ -92,16 +92,16 @@ def test_grouped_gemm_format_errors(lib):
     fake = ctypes.c_void_p(0x1000)
     i64, i32 = ctypes.c_int64, ctypes.c_int32
     # e4m3 intermediate output is only defined for block scales
-    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, i64(128),
+    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, None, i64(128),
                                  i32(8), i32(256), i32(128), 0, 0, 2, fake, fake, None, None)
     assert rc == 1 and "out_format" in _err(lib)
-    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, i64(128),
+    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, None, i64(128),
                                  i32(8), i32(256), i32(96), 1, 0, 0, fake, fake, None, None)
     assert rc == 1 and "inter=96" in _err(lib)
-    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, i64(128),
+    rc = lib.hkmoe_grouped_gemm1(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, None, i64(128),
                                  i32(8), i32(256), i32(128), 1, 5, 0, fake, fake, None, None)
     assert rc == 1 and "w_layout" in _err(lib)
-    rc = lib.hkmoe_grouped_gemm2(fake, fake, fake, fake, fake, fake, i64(128), i32(8), i32(256), i32(128),
+    rc = lib.hkmoe_grouped_gemm2(fake, fake, fake, fake, fake, fake, None, i64(128), i32(8), i32(256), i32(128),
                                  1, 2, fake, None, None)
     assert rc == 1 and "w_layout" in _err(lib)
 
@@ -129,7 +129,8 @@ def _align(x):
 def test_workspace_size_formula(lib, t, e, k, h, i, block):
     r = t * k
     nblk = (t + 31) // 32
-    parts = [r * 4, r * 4, nblk * e * 4, nblk * e * 4, e * 4, (e + 1) * 4, (e + 1) * 4, 4, 16 * 4, r * 4, r * 4]
+    parts = [r * 4, r * 4, nblk * e * 4, nblk * e * 4, e * 4, (e + 1) * 4, (e + 1) * 4,
+             ((r + 255) // 256 + e) * 8, 4, 16 * 4, r * 4, r * 4]
     if not block:
         parts.append(r * i * 2)
     parts += [r * i, r * (i // 128) * 4 if block else 4, r * h * 2]

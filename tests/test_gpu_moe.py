@@ -146,6 +146,43 @@ def test_packed_weights_bit_exact(hk, name):
     assert torch.equal(out.view(torch.int16), ref["out"].view(torch.int16))
 
 
+@pytest.mark.parametrize("name", ["block_e64k8_skew", "tensor_e8k2"])
+def test_mtile_list_order_and_results(hk, name):
+    """The M-tile list holds every (expert, first row) tile exactly once, full
+    256-row tiles first in expert order, then the partial tiles; the grouped
+    GEMMs give the same bits with and without it (it only orders the tiles)."""
+    d = synth.make_moe(seed=21, **SMALL[name])
+    g = moe_inputs_to_gpu(d)
+    r = _run_steps(hk, g, keep_h=False)   # uses the list
+    counts, offs = _np(r["counts"]), _np(r["offsets"])
+    n_mt = int(_np(r["mtile_offsets"])[-1])
+    lst = _np(r["mtile_list"])[:2 * n_mt].reshape(n_mt, 2)
+    full = [(e, offs[e] + 256 * s) for e in range(len(counts)) for s in range(counts[e] // 256)]
+    part = [(e, offs[e] + 256 * (counts[e] // 256)) for e in range(len(counts)) if counts[e] % 256]
+    assert [tuple(x) for x in lst] == full + part
+    # the same layer without the list (expert order): identical intermediates
+    e = len(counts)
+    tc = torch.zeros(16, dtype=torch.int32, device="cuda")
+    block = SMALL[name]["block"]
+    hq2, hs2 = torch.empty_like(r["hq"]), torch.empty_like(r["hs"])
+    if block:
+        hk.tk_kernel.dispatch_grouped_gemm1(g["x_q"], g["x_scale"], r["perm"], g["top_k"], g["w13_q"],
+                                            g["w13_scale"], r["offsets"], r["mtile_offsets"], hq2, hs2, tc[:8])
+    else:
+        h2, amax2 = torch.empty_like(r["h"]), torch.zeros(1, dtype=torch.float32, device="cuda")
+        hk.tk_kernel.dispatch_grouped_gemm1(g["x_q"], g["x_scale"], r["perm"], g["top_k"], g["w13_q"],
+                                            g["w13_scale"], r["offsets"], r["mtile_offsets"], h2, amax2, tc[:8])
+        hk.tk_kernel.dispatch_requant(h2, amax2, hq2, hs2)
+    y2 = torch.empty_like(r["y"])
+    hk.tk_kernel.dispatch_grouped_gemm2(hq2, hs2, g["w2_q"], g["w2_scale"], r["offsets"], r["mtile_offsets"],
+                                        y2, tc[8:])
+    torch.cuda.synchronize()
+    assert torch.equal(hq2.view(torch.uint8), r["hq"].view(torch.uint8))
+    assert torch.equal(hs2, r["hs"])
+    assert torch.equal(y2.view(torch.int16), r["y"].view(torch.int16))
+    del e
+
+
 def test_routing_ties_and_edges(hk):
     """Ties resolve to the lower expert id; T not a multiple of the block; E not a power of 2."""
     rng = np.random.default_rng(3)
