@@ -144,7 +144,11 @@ int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_expert
   HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK,
              "route_topk: top_k=%d outside [1, min(E, %d)]", top_k, kMaxTopK);
   if (num_tokens == 0) return HKMOE_OK;
-  hipLaunchKernelGGL(route_topk_kernel, dim3(route_blocks(num_tokens)), dim3(kRouteThreads), 0,
+  const int chunks = (num_experts + 63) / 64;
+  auto kern = chunks <= 1 ? route_topk_kernel<1> : chunks <= 2 ? route_topk_kernel<2>
+            : chunks <= 4 ? route_topk_kernel<4> : chunks <= 8 ? route_topk_kernel<8>
+                          : route_topk_kernel<16>;
+  hipLaunchKernelGGL(kern, dim3(route_blocks(num_tokens)), dim3(kTopkThreads), 0,
                      static_cast<hipStream_t>(stream), logits, static_cast<int>(num_tokens),
                      num_experts, top_k, topk_idx, topk_w, block_counts);
   return check_launch("route_topk_kernel");

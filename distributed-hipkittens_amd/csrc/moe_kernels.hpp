@@ -13,7 +13,8 @@
 namespace hkmoe {
 
 constexpr int kRouteTok = 32;      // tokens per routing/scatter workgroup
-constexpr int kRouteThreads = 256; // 4 waves, 8 tokens each
+constexpr int kRouteThreads = 256; // scatter: 4 waves per 32-token block
+constexpr int kTopkThreads = 1024; // top-k: 16 waves, 2 tokens each
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kScanThreads = 1024;
@@ -26,28 +27,29 @@ __device__ __forceinline__ bool route_better(float av, int ai, float bv, int bi)
 }
 
 // ---------------------------------------------------------------------------
-// 1. top-k + softmax + per-block histogram.  One wave per token.
+// 1. top-k + softmax + per-block histogram.  One wave per token; CH = number
+//    of 64-expert chunks a lane holds (power of two >= ceil(E / 64)).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kRouteThreads) void route_topk_kernel(
+template <int CH>
+__global__ __launch_bounds__(kTopkThreads) void route_topk_kernel(
     const float* __restrict__ logits, int num_tokens, int num_experts, int top_k,
     int32_t* __restrict__ topk_idx, float* __restrict__ topk_w, int32_t* __restrict__ block_counts) {
   __shared__ int hist[kMaxExperts];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  for (int e = threadIdx.x; e < num_experts; e += kRouteThreads) hist[e] = 0;
+  for (int e = threadIdx.x; e < num_experts; e += kTopkThreads) hist[e] = 0;
   __syncthreads();
 
-  const int chunks = (num_experts + 63) >> 6;
   const int t0 = blockIdx.x * kRouteTok;
-  for (int tt = wave; tt < kRouteTok; tt += kRouteThreads / 64) {
+  for (int tt = wave; tt < kRouteTok; tt += kTopkThreads / 64) {
     const int t = t0 + tt;
     if (t >= num_tokens) break;
     const float* row = logits + static_cast<int64_t>(t) * num_experts;
-    float v[kMaxExperts / 64];
+    float v[CH];
 #pragma unroll
-    for (int c = 0; c < kMaxExperts / 64; ++c) {
+    for (int c = 0; c < CH; ++c) {
       const int id = c * 64 + lane;
-      v[c] = (c < chunks && id < num_experts) ? row[id] : 0.0f;
+      v[c] = (id < num_experts) ? row[id] : 0.0f;
     }
     uint32_t taken = 0;
     float my_v = 0.0f, v0 = 0.0f;
@@ -56,9 +58,9 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_kernel(
       float bv = 0.0f;
       int bi = -1;
 #pragma unroll
-      for (int c = 0; c < kMaxExperts / 64; ++c) {
+      for (int c = 0; c < CH; ++c) {
         const int id = c * 64 + lane;
-        if (c < chunks && id < num_experts && !((taken >> c) & 1u) && route_better(v[c], id, bv, bi)) {
+        if (id < num_experts && !((taken >> c) & 1u) && route_better(v[c], id, bv, bi)) {
           bv = v[c];
           bi = id;
         }
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_topk_kernel(
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < num_experts; e += kRouteThreads)
+  for (int e = threadIdx.x; e < num_experts; e += kTopkThreads)
     block_counts[static_cast<int64_t>(blockIdx.x) * num_experts + e] = hist[e];
 }
 
