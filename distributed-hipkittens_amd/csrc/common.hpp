@@ -96,8 +96,14 @@ __device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> two bf16 (lo in bits 0-15), round to nearest even: one
+// v_cvt_pk_bf16_f32 (same bits as bf16_rne_bits for every non-NaN input).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return bf16_rne_bits(lo) | (bf16_rne_bits(hi) << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // fp32 -> OCP e4m3fn byte: round to nearest even, saturate to +-448,
@@ -116,6 +122,18 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   // normal: keep 3 mantissa bits with RNE on the 20 dropped bits
   const uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;
   return sign | (r - (120u << 3));  // rebias exponent 127 -> 7
+}
+
+// e4m3(fl(x / s)) for finite x and a positive normal s, with inv = fl(1 / s).
+// y = fl(x * inv) is within 2 ulp of the correctly rounded quotient, so both
+// round to the same e4m3 value unless y lies within 8 ulp of an e4m3 rounding
+// midpoint (dropped 20 mantissa bits near 0x80000) or below the e4m3 normal
+// range (2^-6, where the rounding step changes); only those lanes divide.
+__device__ __forceinline__ uint32_t e4m3_quot(float x, float s, float inv) {
+  float y = x * inv;
+  const uint32_t a = f32_bits(y) & 0x7fffffffu;
+  if (a < 0x3c800000u || ((a & 0xfffffu) - 0x7fff8u) < 16u) y = x / s;
+  return f32_to_e4m3(y);
 }
 
 __device__ __forceinline__ float e4m3_to_f32(uint32_t q) {

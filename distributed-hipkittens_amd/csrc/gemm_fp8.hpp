@@ -126,7 +126,11 @@ __device__ __forceinline__ i32x8 read_frag(const uint8_t* tile, int row, int hal
   return r;
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+// silu(g) = g / (1 + e^-g) with the hardware exp2 and reciprocal (a few ulp;
+// the result is rounded to bf16 next).
+__device__ __forceinline__ float silu(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
 
 // Tile row of activation-scale slot s: the lane with l16 = r % 16 of wave-row
 // r / 128 reads its 8 sub-tile scales as 8 consecutive floats.
@@ -498,13 +502,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
             const float fg = fac(i, 0), fu = fac(i, 1);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-              uint32_t hb[4];
+              float hv[4];
 #pragma unroll
-              for (int q = 0; q < 4; ++q)
-                hb[q] = bf16_rne_bits(silu(acc[i][j][q] * fg) * (acc[i][j + 2][q] * fu));
+              for (int q = 0; q < 4; ++q) hv[q] = silu(acc[i][j][q] * fg) * (acc[i][j + 2][q] * fu);
               uint2 v;
-              v.x = hb[0] | (hb[1] << 16);
-              v.y = hb[2] | (hb[3] << 16);
+              v.x = pack_bf16x2(hv[0], hv[1]);
+              v.y = pack_bf16x2(hv[2], hv[3]);
               *reinterpret_cast<uint2*>(crow + wg * 32 + j * 16 + lg * 4) = v;
             }
           } else {
@@ -558,6 +561,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
           m = fmaxf(m, __shfl_xor(m, 1, 64));
           if (r < valid) {
             const float s = scale_from_amax(m);
+            const float inv = 1.0f / s;
             uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * 128 + half * 64;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -569,10 +573,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
                   const uint32_t lo = w[2 * q], hi = w[2 * q + 1];
-                  qw[h2 * 2 + q] = f32_to_e4m3(bf16_bits_to_f32(lo & 0xffffu) / s) |
-                                   (f32_to_e4m3(bf16_bits_to_f32(lo >> 16) / s) << 8) |
-                                   (f32_to_e4m3(bf16_bits_to_f32(hi & 0xffffu) / s) << 16) |
-                                   (f32_to_e4m3(bf16_bits_to_f32(hi >> 16) / s) << 24);
+                  qw[h2 * 2 + q] = e4m3_quot(bf16_bits_to_f32(lo & 0xffffu), s, inv) |
+                                   (e4m3_quot(bf16_bits_to_f32(lo >> 16), s, inv) << 8) |
+                                   (e4m3_quot(bf16_bits_to_f32(hi & 0xffffu), s, inv) << 16) |
+                                   (e4m3_quot(bf16_bits_to_f32(hi >> 16), s, inv) << 24);
                 }
               }
               *reinterpret_cast<uint4*>(dst + u * 16) = uint4{qw[0], qw[1], qw[2], qw[3]};

@@ -297,7 +297,8 @@ __global__ __launch_bounds__(256) void requant_group_kernel(const uint16_t* __re
     const float a = bf16_bits_to_f32(pair & 0xffffu), b = bf16_bits_to_f32(pair >> 16);
     const float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
     const float s = scale_from_amax(amax);
-    const uint32_t q = f32_to_e4m3(a / s) | (f32_to_e4m3(b / s) << 8);
+    const float inv = 1.0f / s;
+    const uint32_t q = e4m3_quot(a, s, inv) | (e4m3_quot(b, s, inv) << 8);
     *reinterpret_cast<uint16_t*>(hq + base) = static_cast<uint16_t>(q);
     if (lane == 0) hs_t[static_cast<int64_t>(g) * rows + r] = s;
   }
@@ -309,6 +310,7 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
                                                              uint8_t* __restrict__ hq,
                                                              float* __restrict__ hs) {
   const float s = scale_from_amax(*amax);
+  const float inv = 1.0f / s;
   if (blockIdx.x == 0 && threadIdx.x == 0) hs[0] = s;
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n8; i += static_cast<int64_t>(gridDim.x) * 256) {
     const uint4 v = reinterpret_cast<const uint4*>(h)[i];
@@ -321,8 +323,8 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const uint32_t pr = w[q * 2 + u];
-        acc |= f32_to_e4m3(bf16_bits_to_f32(pr & 0xffffu) / s) << (16 * u);
-        acc |= f32_to_e4m3(bf16_bits_to_f32(pr >> 16) / s) << (16 * u + 8);
+        acc |= e4m3_quot(bf16_bits_to_f32(pr & 0xffffu), s, inv) << (16 * u);
+        acc |= e4m3_quot(bf16_bits_to_f32(pr >> 16), s, inv) << (16 * u + 8);
       }
       op[q] = acc;
     }

@@ -183,6 +183,44 @@ def test_mtile_list_order_and_results(hk, name):
     del e
 
 
+@pytest.mark.parametrize("block", [True, False])
+def test_requant_large_bit_exact(hk, block):
+    """Requantisation of 8M bf16 values (log-normal row magnitudes, plus rows
+    whose values sit on and next to e4m3 rounding midpoints) is bit-exact
+    against the oracle: the quotient x / s is taken as a product with 1 / s
+    except near midpoints, and this exercises both paths."""
+    rng = np.random.default_rng(31)
+    rows, inter = 4096, 2048
+    h = rng.standard_normal((rows, inter)).astype(np.float32)
+    h *= np.exp(rng.standard_normal((rows, 1)) * 3).astype(np.float32)
+    # row 0: amax 448 (scale exactly 1): every e4m3 midpoint and its bf16 neighbours
+    codes = np.arange(1, 0x7E, dtype=np.uint8)
+    v = spec.dequant_per_tensor(codes, np.float32(1.0)).astype(np.float32)
+    mid = ((v[:-1] + v[1:]) / 2).astype(np.float32)
+    near = np.concatenate([mid, np.nextafter(mid, np.float32(0)), np.nextafter(mid, np.float32(1e9))])
+    near = spec.bf16_round(near)
+    row = np.resize(np.concatenate([near, -near]), inter).astype(np.float32)
+    row[0] = 448.0
+    h[0] = row
+    h = spec.bf16_round(h)
+    hb = torch.from_numpy(h).to(torch.bfloat16).cuda()
+    hq = torch.empty((rows, inter), dtype=torch.float8_e4m3fn, device="cuda")
+    if block:
+        hs = torch.empty((inter // 128, rows), dtype=torch.float32, device="cuda")
+        hk.tk_kernel.dispatch_requant(hb, None, hq, hs)
+    else:
+        hs = torch.empty(1, dtype=torch.float32, device="cuda")
+        amax = torch.tensor([float(np.abs(h).max())], dtype=torch.float32, device="cuda")
+        hk.tk_kernel.dispatch_requant(hb, amax, hq, hs)
+    torch.cuda.synchronize()
+    q_ref, s_ref = spec.requant(h, block)
+    np.testing.assert_array_equal(f8_np(hq), q_ref)
+    if block:
+        np.testing.assert_array_equal(_np(hs).T, s_ref)
+    else:
+        assert _np(hs)[0] == s_ref
+
+
 def test_routing_ties_and_edges(hk):
     """Ties resolve to the lower expert id; T not a multiple of the block; E not a power of 2."""
     rng = np.random.default_rng(3)
