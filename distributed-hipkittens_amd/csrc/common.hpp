@@ -124,16 +124,30 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   return sign | (r - (120u << 3));  // rebias exponent 127 -> 7
 }
 
-// e4m3(fl(x / s)) for finite x and a positive normal s, with inv = fl(1 / s).
-// y = fl(x * inv) is within 2 ulp of the correctly rounded quotient, so both
-// round to the same e4m3 value unless y lies within 8 ulp of an e4m3 rounding
-// midpoint (dropped 20 mantissa bits near 0x80000) or below the e4m3 normal
-// range (2^-6, where the rounding step changes); only those lanes divide.
-__device__ __forceinline__ uint32_t e4m3_quot(float x, float s, float inv) {
-  float y = x * inv;
+// fl(x / s) as far as its e4m3 rounding goes, for finite x and a positive
+// normal s, with inv = fl(1 / s).  y = fl(x * inv) is within 2 ulp of the
+// correctly rounded quotient, so both round to the same e4m3 value unless y
+// lies within 8 ulp of an e4m3 rounding midpoint (dropped 20 mantissa bits
+// near 0x80000) or below the e4m3 normal range (2^-6, where the rounding step
+// changes); only those lanes divide.
+__device__ __forceinline__ float quot_e4m3(float x, float s, float inv) {
+  const float y = x * inv;
   const uint32_t a = f32_bits(y) & 0x7fffffffu;
-  if (a < 0x3c800000u || ((a & 0xfffffu) - 0x7fff8u) < 16u) y = x / s;
-  return f32_to_e4m3(y);
+  return (a < 0x3c800000u || ((a & 0xfffffu) - 0x7fff8u) < 16u) ? x / s : y;
+}
+
+// Four finite fp32 -> four e4m3fn bytes (a in bits 0-7), round to nearest
+// even, saturating at +-448: a clamp to [-448, 448] and two hardware packed
+// conversions.  (The conversion alone rounds exactly like f32_to_e4m3 for
+// |v| <= 448 but gives NaN above 464 instead of saturating; the clamp makes the
+// two agree on every finite input.)
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
+  const float lo = -448.0f, hi = 448.0f;
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(a, lo, hi),
+                                          __builtin_amdgcn_fmed3f(b, lo, hi), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(c, lo, hi),
+                                      __builtin_amdgcn_fmed3f(d, lo, hi), w, true);
+  return static_cast<uint32_t>(w);
 }
 
 __device__ __forceinline__ float e4m3_to_f32(uint32_t q) {

@@ -573,10 +573,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
                   const uint32_t lo = w[2 * q], hi = w[2 * q + 1];
-                  qw[h2 * 2 + q] = e4m3_quot(bf16_bits_to_f32(lo & 0xffffu), s, inv) |
-                                   (e4m3_quot(bf16_bits_to_f32(lo >> 16), s, inv) << 8) |
-                                   (e4m3_quot(bf16_bits_to_f32(hi & 0xffffu), s, inv) << 16) |
-                                   (e4m3_quot(bf16_bits_to_f32(hi >> 16), s, inv) << 24);
+                  qw[h2 * 2 + q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(lo & 0xffffu), s, inv),
+                                               quot_e4m3(bf16_bits_to_f32(lo >> 16), s, inv),
+                                               quot_e4m3(bf16_bits_to_f32(hi & 0xffffu), s, inv),
+                                               quot_e4m3(bf16_bits_to_f32(hi >> 16), s, inv));
                 }
               }
               *reinterpret_cast<uint4*>(dst + u * 16) = uint4{qw[0], qw[1], qw[2], qw[3]};

@@ -298,7 +298,7 @@ __global__ __launch_bounds__(256) void requant_group_kernel(const uint16_t* __re
     const float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
     const float s = scale_from_amax(amax);
     const float inv = 1.0f / s;
-    const uint32_t q = e4m3_quot(a, s, inv) | (e4m3_quot(b, s, inv) << 8);
+    const uint32_t q = pack_e4m3x4(quot_e4m3(a, s, inv), quot_e4m3(b, s, inv), 0.0f, 0.0f) & 0xffffu;
     *reinterpret_cast<uint16_t*>(hq + base) = static_cast<uint16_t>(q);
     if (lane == 0) hs_t[static_cast<int64_t>(g) * rows + r] = s;
   }
@@ -319,14 +319,11 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
     uint32_t* op = &o.x;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      uint32_t acc = 0;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const uint32_t pr = w[q * 2 + u];
-        acc |= e4m3_quot(bf16_bits_to_f32(pr & 0xffffu), s, inv) << (16 * u);
-        acc |= e4m3_quot(bf16_bits_to_f32(pr >> 16), s, inv) << (16 * u + 8);
-      }
-      op[q] = acc;
+      const uint32_t p0 = w[q * 2], p1 = w[q * 2 + 1];
+      op[q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(p0 & 0xffffu), s, inv),
+                          quot_e4m3(bf16_bits_to_f32(p0 >> 16), s, inv),
+                          quot_e4m3(bf16_bits_to_f32(p1 & 0xffffu), s, inv),
+                          quot_e4m3(bf16_bits_to_f32(p1 >> 16), s, inv));
     }
     reinterpret_cast<uint2*>(hq)[i] = o;
   }
