@@ -213,8 +213,9 @@ def _kernel_label(name):
     if "gemm_fp8_persistent" in name:
         epi = name.split("Epi)")[1][0] if "Epi)" in name else "?"
         return "grouped_gemm1" if epi in "23" else "grouped_gemm2"
-    if name.startswith("hkmoe::"):
-        return name[len("hkmoe::"):].split("(")[0].replace("_kernel", "")
+    n = name[len("void "):] if name.startswith("void ") else name  # template kernels
+    if n.startswith("hkmoe::"):
+        return n[len("hkmoe::"):].split("(")[0].split("<")[0].replace("_kernel", "")
     return None
 
 
