@@ -525,4 +525,66 @@ int hkmoe_quant_tensor(const float* x, int64_t rows, int64_t cols, void* q, floa
   return check_launch("quant_tensor_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// MX (e8m0 1x32) operands and GEMM
+// ---------------------------------------------------------------------------
+int hkmoe_quant_mx(const float* x, int64_t rows, int64_t cols, void* q, void* s, hkmoe_stream_t stream) {
+  HK_REQUIRE(x && q && s, "quant_mx: null pointer");
+  HK_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, "quant_mx: cols=%lld must be a positive multiple of 32",
+             (long long)cols);
+  const int64_t blocks = rows * (cols / 32);
+  if (blocks == 0) return HKMOE_OK;
+  const int grid = static_cast<int>(std::min<int64_t>((blocks * 8 + 255) / 256, 8192));
+  hipLaunchKernelGGL(quant_mx_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), x, blocks,
+                     static_cast<uint8_t*>(q), static_cast<uint8_t*>(s));
+  return check_launch("quant_mx_kernel");
+}
+
+int hkmoe_mx_pack_scales(const void* s, int64_t rows, int64_t cols, void* packed, hkmoe_stream_t stream) {
+  HK_REQUIRE(s && packed, "mx_pack_scales: null pointer");
+  HK_REQUIRE(rows >= 0 && cols > 0 && cols % kBK == 0,
+             "mx_pack_scales: cols=%lld must be a positive multiple of 128", (long long)cols);
+  const int64_t rows64 = (rows + 63) / 64 * 64;
+  const int64_t words = (cols / kBK) * rows64;
+  if (words == 0) return HKMOE_OK;
+  const int grid = static_cast<int>(std::min<int64_t>((words + 255) / 256, 8192));
+  hipLaunchKernelGGL(mx_pack_scales_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint8_t*>(s), rows, cols / 32, rows64, static_cast<uint32_t*>(packed),
+                     words);
+  return check_launch("mx_pack_scales_kernel");
+}
+
+int hkmoe_gemm_mx(const void* a, const void* a_scale, const void* b, const void* b_scale, void* c, int64_t m,
+                  int64_t n, int64_t k, int out_dtype, hkmoe_stream_t stream) {
+  HK_REQUIRE(a && a_scale && b && b_scale && c, "gemm_mx: null pointer");
+  HK_REQUIRE(m >= 0 && n > 0 && k > 0, "gemm_mx: bad shape M=%lld N=%lld K=%lld", (long long)m, (long long)n,
+             (long long)k);
+  HK_REQUIRE(k % kBK == 0, "gemm_mx: K=%lld must be a multiple of 128", (long long)k);
+  HK_REQUIRE(n % kBN == 0, "gemm_mx: N=%lld must be a multiple of 256", (long long)n);
+  const int64_t m64 = (m + 63) / 64 * 64;
+  HK_REQUIRE(k <= (1 << 20) && n * k < (1ll << 32) && m < (1ll << 31) && m64 * (k / 32) < (1ll << 32) &&
+                 n * (k / 32) < (1ll << 32),
+             "gemm_mx: operand too large for 32-bit buffer offsets");
+  HK_REQUIRE(out_dtype == HKMOE_BF16 || out_dtype == HKMOE_F32, "gemm_mx: bad out_dtype %d", out_dtype);
+  if (m == 0) return HKMOE_OK;
+  GemmParams p{};
+  p.a = static_cast<const uint8_t*>(a);
+  p.b = static_cast<const uint8_t*>(b);
+  p.c = c;
+  p.a_scale = static_cast<const float*>(a_scale);
+  p.b_scale = static_cast<const float*>(b_scale);
+  p.rows = m;
+  p.a_rows = m;
+  p.as_rs = m64;
+  p.num_experts = 1;
+  p.K = static_cast<int32_t>(k);
+  p.nb = static_cast<int32_t>(n);
+  p.n_out = static_cast<int32_t>(n);
+  p.n_tiles = static_cast<int32_t>(n / kBN);
+  p.blk_m_log2 = 2;  // 4 x 8 tile blocks
+  auto st = static_cast<hipStream_t>(stream);
+  return out_dtype == HKMOE_BF16 ? launch_gemm<Epi::kStoreBf16, Scale::kMX>(p, st)
+                                 : launch_gemm<Epi::kStoreF32, Scale::kMX>(p, st);
+}
+
 }  // extern "C"

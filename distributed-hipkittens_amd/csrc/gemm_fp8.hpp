@@ -33,6 +33,16 @@
 //    i.e. one multiply of the accumulator before the block's MFMA (no
 //    MFMA -> VALU dependency, no partial-sum registers).  Scales must be
 //    positive normal fp32 numbers (the quantisers floor them at 2^-126).
+//  * MX (OCP microscaling) mode: 1x32 e8m0 exponents per row of A and of B,
+//    applied inside the MFMA (v_mfma_scale_f32_16x16x128_f8f6f4), which takes
+//    the exponent of row l%16 and K block l/16 from lane l: one e8m0 byte per
+//    lane and operand, picked from a 32-bit word by the instruction's op_sel
+//    (fragments are read in the instruction's K order, read_frag_mx).  The
+//    scales arrive pre-packed so that word (k step kt, position p) of a 64-row
+//    group holds, in byte g, the exponent of row 16g + p%16 of the group for K
+//    block 4kt + (p%64)/16 (mx_pack_scales_kernel); a wave's words for one
+//    64-row group are then 64 consecutive words, DMA'd with the A half (they
+//    add 2 KiB to a stage) and read as one dword per lane: no VALU rescale.
 //  * optional row gather: A row of output row p is a_gather[p] / gather_div
 //    (the expert-sorted permutation), so GEMM 1 reads token rows in place.
 //  * MFMA operands are swapped (B fragment as src0) so each lane owns 4
@@ -64,7 +74,7 @@
 namespace hkmoe {
 
 enum class Epi : int { kStoreBf16 = 0, kStoreF32 = 1, kSiluBf16 = 2, kSiluQuant = 3 };
-enum class Scale : int { kTensor = 0, kBlock = 1 };
+enum class Scale : int { kTensor = 0, kBlock = 1, kMX = 2 };
 
 struct GemmParams {
   const uint8_t* a;            // A rows [a_rows, K] e4m3
@@ -72,7 +82,9 @@ struct GemmParams {
   const uint8_t* b;            // [E, nb, K] e4m3, row-major or packed (b_packed)
   void* c;                     // [rows, n_out]: bf16, fp32 or (kSiluQuant) e4m3
   const float* a_scale;        // kTensor: [1] or null (1.0); kBlock: a_scale[r*as_rs + kb*as_ks]
+                               // kMX: packed e8m0 words [K/128][as_rs] (as_rs = rows rounded up to 64)
   const float* b_scale;        // kTensor: [E] or null (1.0); kBlock: [E, nb/128, K/128]
+                               // kMX: packed e8m0 words [K/128][nb]
   float* c_scale;              // kSiluQuant: group scales, transposed [n_out/128, rows]
   const int32_t* offsets;      // [E+1] row offsets; nullptr = dense (one segment of `rows`)
   const int32_t* mtile_offsets;// [E+1] M-tile offsets; nullptr = dense
@@ -126,6 +138,28 @@ __device__ __forceinline__ i32x8 read_frag(const uint8_t* tile, int row, int hal
   return r;
 }
 
+// The same fragment in the scaled MFMA's K order, which the e8m0 scales need
+// (the unscaled instruction accepts any common order of both operands): lane
+// l holds K bytes 16g .. 16g+15 in registers 0-3 and 64+16g .. 64+16g+15 in
+// registers 4-7 (g = l/16), so 32-byte K block b lies in lane groups 2(b%2)
+// and 2(b%2)+1, and the instruction takes block b's exponent for row l%16 from
+// lane group b.
+__device__ __forceinline__ i32x8 read_frag_mx(const uint8_t* tile, int row, int lg, int x) {
+  const uint8_t* base = tile + row * kBK;
+  const i32x4 lo = *reinterpret_cast<const i32x4*>(base + (lg ^ x) * 16);
+  const i32x4 hi = *reinterpret_cast<const i32x4*>(base + ((lg + 4) ^ x) * 16);
+  i32x8 r;
+  r.s0 = lo.x; r.s1 = lo.y; r.s2 = lo.z; r.s3 = lo.w;
+  r.s4 = hi.x; r.s5 = hi.y; r.s6 = hi.z; r.s7 = hi.w;
+  return r;
+}
+
+template <bool MX>
+__device__ __forceinline__ i32x8 read_operand(const uint8_t* tile, int row, int lg, int x) {
+  if constexpr (MX) return read_frag_mx(tile, row, lg, x);
+  else return read_frag(tile, row, lg, x);
+}
+
 // silu(g) = g / (1 + e^-g) with the hardware exp2 and reciprocal (a few ulp;
 // the result is rounded to bf16 next).
 __device__ __forceinline__ float silu(float g) {
@@ -137,6 +171,24 @@ __device__ __forceinline__ float silu(float g) {
 __device__ __forceinline__ int scale_slot_row(int slot) {
   const int wm = slot >> 7, w = slot & 127;
   return wm * 128 + (w & 7) * 16 + (w >> 3);
+}
+
+// Scaled MFMA with e8m0 operand scales: byte OPB of sb scales the B fragment
+// (src0), byte OPA of sa the A fragment (src1); e4m3 operands.
+template <int OPB, int OPA>
+__device__ __forceinline__ f32x4 mfma_mx(const i32x8& b, const i32x8& a, f32x4 c, int sb, int sa) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b, a, c, 0, 0, OPB, sb, OPA, sa);
+}
+
+// One A sub-tile (16 rows, exponent byte U of sa) against the wave's four B
+// fragments (exponent bytes 0-3 of sb).
+template <int U>
+__device__ __forceinline__ void mx_subtile(f32x4 (&acc)[4], const i32x8 (&bf)[4], const i32x8& af,
+                                           int sb, int sa) {
+  acc[0] = mfma_mx<0, U>(bf[0], af, acc[0], sb, sa);
+  acc[1] = mfma_mx<1, U>(bf[1], af, acc[1], sb, sa);
+  acc[2] = mfma_mx<2, U>(bf[2], af, acc[2], sb, sa);
+  acc[3] = mfma_mx<3, U>(bf[3], af, acc[3], sb, sa);
 }
 
 // Wait for this wave's outstanding DMA and LDS reads, then the workgroup
@@ -155,7 +207,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   float* bs_lds = reinterpret_cast<float*>(smem + 2 * kStageBytes);  // [2][k_blocks]
 
   constexpr bool kBlockSc = (SC == Scale::kBlock);
+  constexpr bool kMX = (SC == Scale::kMX);
   constexpr bool kSilu = (EPI == Epi::kSiluBf16 || EPI == Epi::kSiluQuant);
+  // stage: A tile, B tile, A scales (1 KiB) and, in MX mode, B scales (1 KiB)
+  constexpr int kStg = kMX ? kStageBytes + kScaleBytes : kStageBytes;
+  static_assert(!(kMX && kSilu), "MX scales are for the plain-store GEMM");
+  static_assert(2 * kStg <= kLdsData, "LDS budget");
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -293,6 +350,25 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       const int ar = p.a_gather ? p.a_gather[rr] / p.gather_div : rr;
       as_voff = static_cast<int>(ar * p.as_rs) * 4;
     }
+    // MX: every wave DMAs one 64-word group per step -- waves 0-1 of a group
+    // the A words of its half, waves 2-3 the B words of rows 128*grp .. +127.
+    // Words past the packed arrays read as zero (rows that are never stored).
+    i32x4 mx_srd;
+    int mx_voff = 0, mx_kstride = 0, mx_lds = 0;
+    if constexpr (kMX) {
+      const int k_steps_ = p.K / kBK;
+      if (wg < 2) {
+        mx_srd = make_srd(p.a_scale, static_cast<uint32_t>(k_steps_ * p.as_rs * 4));
+        mx_voff = (row0 + wave_row0 + wg * 64 + lane) * 4;
+        mx_kstride = static_cast<int>(p.as_rs) * 4;
+        mx_lds = 2 * kTileBytes + (wave_row0 + wg * 64) * 4;
+      } else {
+        mx_srd = make_srd(p.b_scale, static_cast<uint32_t>(k_steps_ * p.nb * 4));
+        mx_voff = (nt * kBN + grp * 128 + (wg - 2) * 64 + lane) * 4;
+        mx_kstride = p.nb * 4;
+        mx_lds = 2 * kTileBytes + kScaleBytes + (grp * 128 + (wg - 2) * 64) * 4;
+      }
+    }
 
     // DMA instructions of one K step issued by this wave.  issue_a: its
     // group's A half (4, dead 16-row sub-tiles skipped) and, for waves 0-1 of
@@ -300,7 +376,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     // of the B stage (group 0 rows 0-127, group 1 rows 128-255); being the
     // last 4 loads a wave issues, they are what vmcnt(4) leaves in flight.
     auto issue_a = [&](int kt) {
-      uint8_t* sa = smem + (kt & 1) * kStageBytes;
+      uint8_t* sa = smem + (kt & 1) * kStg;
       const int koff = kt * kBK;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -312,9 +388,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         load_lds_4B(as_srd, sa + 2 * kTileBytes + (wave_row0 + wg * 64) * 4, as_voff,
                     static_cast<int>(kt * p.as_ks) * 4);
       }
+      if constexpr (kMX) load_lds_4B(mx_srd, sa + mx_lds, mx_voff, kt * mx_kstride);
     };
     auto issue_b = [&](int kt) {
-      uint8_t* sb = smem + (kt & 1) * kStageBytes + kTileBytes;
+      uint8_t* sb = smem + (kt & 1) * kStg + kTileBytes;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int i = grp * 4 + q;
@@ -377,16 +454,25 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     // memory phase).
     for (int kt = 0; kt < k_steps; ++kt) {
       const bool more = kt + 1 < k_steps;
-      const uint8_t* sa = smem + (kt & 1) * kStageBytes;
+      const uint8_t* sa = smem + (kt & 1) * kStg;
       const uint8_t* sb = sa + kTileBytes;
 
       // ---- memory phase 1: B fragments, A sub-tiles 0-3, scales, DMA kt+1
       i32x8 bf[4], af[4];
+      int mx_sb = 0, mx_sa0 = 0, mx_sa1 = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = read_frag(sb, wg * 64 + j * 16 + l16, lg, fx);
+      for (int j = 0; j < 4; ++j) bf[j] = read_operand<kMX>(sb, wg * 64 + j * 16 + l16, lg, fx);
+      if constexpr (kMX) {
+        // exponent words: B rows wg*64 + 16j + l16 (byte j), A rows of
+        // sub-tiles 0-3 and 4-7 (byte i % 4), all for K block 4kt + lg
+        const int* sw = reinterpret_cast<const int*>(sb + kTileBytes);
+        mx_sa0 = sw[wave_row0 + lane];
+        mx_sa1 = sw[wave_row0 + 64 + lane];
+        mx_sb = sw[kBM + wg * 64 + lane];
+      }
       if (live_sub > 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = read_frag(sa, wave_row0 + i * 16 + l16, lg, fx);
+        for (int i = 0; i < 4; ++i) af[i] = read_operand<kMX>(sa, wave_row0 + i * 16 + l16, lg, fx);
       }
       if constexpr (kBlockSc) {
         // this step's scales; the factors are formed in the compute phases
@@ -431,11 +517,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         // Skipped only when all four sub-tiles are dead; a partly live phase
         // also computes its dead sub-tiles (stale fragments, never stored).
         if (live_sub > i0) {
+          if constexpr (kMX) {
+            const int sa_w = i0 == 0 ? mx_sa0 : mx_sa1;
+            mx_subtile<0>(acc[i0 + 0], bf, af[0], mx_sb, sa_w);
+            mx_subtile<1>(acc[i0 + 1], bf, af[1], mx_sb, sa_w);
+            mx_subtile<2>(acc[i0 + 2], bf, af[2], mx_sb, sa_w);
+            mx_subtile<3>(acc[i0 + 3], bf, af[3], mx_sb, sa_w);
+          } else {
 #pragma unroll
-          for (int t = 0; t < 16; ++t) {
-            const int u = t >> 2, j = t & 3;
-            if constexpr (kBlockSc) acc[i0 + u][j] *= (kSilu && j >= 2) ? r1[u] : r0[u];
-            acc[i0 + u][j] = mfma_e4m3_16x16x128(bf[j], af[u], acc[i0 + u][j]);
+            for (int t = 0; t < 16; ++t) {
+              const int u = t >> 2, j = t & 3;
+              if constexpr (kBlockSc) acc[i0 + u][j] *= (kSilu && j >= 2) ? r1[u] : r0[u];
+              acc[i0 + u][j] = mfma_e4m3_16x16x128(bf[j], af[u], acc[i0 + u][j]);
+            }
           }
         }
         __builtin_amdgcn_s_setprio(0);
@@ -448,7 +542,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       // ---- memory phase 2: A sub-tiles 4-7
       if (live_sub > 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = read_frag(sa, wave_row0 + (i + 4) * 16 + l16, lg, fx);
+        for (int i = 0; i < 4; ++i) af[i] = read_operand<kMX>(sa, wave_row0 + (i + 4) * 16 + l16, lg, fx);
       }
       const bool more2 = kt + 2 < k_steps;
       if (more2) issue_b(kt + 2);
@@ -467,7 +561,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     // lane holds, for sub-tile i and n fragment j, output row wave_row0+16i+l16
     // and columns 16*j + 4*lg .. +3 of the wave's 64-column quarter
     float tens = 1.0f;
-    if constexpr (!kBlockSc) tens = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
+    if constexpr (SC == Scale::kTensor)
+      tens = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
     auto fac = [&](int i, int h) -> float {
       if constexpr (kBlockSc) return sa_prev[i] * (h ? sb_prev1 : sb_prev0);
       else return tens;

@@ -439,4 +439,55 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const float* __restri
     q[i] = static_cast<uint8_t>(f32_to_e4m3(x[i] / sc));
 }
 
+// ---------------------------------------------------------------------------
+// 7. MX (e8m0 1x32) operands
+// ---------------------------------------------------------------------------
+// x viewed as [blocks, 32] (row-major [R, C] with C % 32 == 0): 8 lanes per
+// block, 4 elements each.  s = biased exponent of amax = clamp(floor(log2 amax)
+// + 127, 0, 254) -- exact for every finite amax (0 for zero or subnormal amax)
+// -- and q = e4m3(x * 2^(127 - s)), an exact power-of-two scaling followed by
+// one RNE conversion (|x * 2^(127-s)| < 2, so the saturating clamp never acts).
+// Reference behaviour: 4_wave.cu:296-321, 368-373.
+__global__ __launch_bounds__(256) void quant_mx_kernel(const float* __restrict__ x, int64_t blocks,
+                                                       uint8_t* __restrict__ q, uint8_t* __restrict__ s) {
+  const int64_t quads = blocks * 8;
+  // quad i = lane i % 8 of block i / 8; the 8 lanes of a block sit in one wave
+  // (i % 8 == threadIdx.x % 8) and pass the loop test together
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < quads; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, __shfl_xor(m, 1, kWave));
+    m = fmaxf(m, __shfl_xor(m, 2, kWave));
+    m = fmaxf(m, __shfl_xor(m, 4, kWave));
+    const uint32_t e = min((__float_as_uint(m) >> 23) & 0xffu, 254u);
+    const int sh = 127 - static_cast<int>(e);
+    *reinterpret_cast<uint32_t*>(q + 4 * i) =
+        pack_e4m3x4(__builtin_amdgcn_ldexpf(v.x, sh), __builtin_amdgcn_ldexpf(v.y, sh),
+                    __builtin_amdgcn_ldexpf(v.z, sh), __builtin_amdgcn_ldexpf(v.w, sh));
+    if ((i & 7) == 0) s[i >> 3] = static_cast<uint8_t>(e);
+  }
+}
+
+// e8m0 s [R, C/32] -> packed words [C/128, R64] (R64 = R rounded up to 64):
+// word (kt, p) byte g = s[64*(p/64) + 16*g + p%16][4*kt + (p%64)/16], 0 past
+// row R.  One thread per word.  Same words as the reference's pack_scales_kernel
+// + repack_scales_for_mfma_kernel (4_wave.cu:323-364) when R % 64 == 0.
+__global__ __launch_bounds__(256) void mx_pack_scales_kernel(const uint8_t* __restrict__ s, int64_t rows,
+                                                             int64_t kblocks, int64_t rows64,
+                                                             uint32_t* __restrict__ packed,
+                                                             int64_t words) {
+  for (int64_t w = blockIdx.x * 256ll + threadIdx.x; w < words; w += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t kt = w / rows64, p = w - kt * rows64;
+    const int64_t r0 = (p & ~63ll) + (p & 15);
+    const int64_t kb = 4 * kt + ((p >> 4) & 3);
+    uint32_t v = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t r = r0 + 16 * g;
+      if (r < rows) v |= static_cast<uint32_t>(s[r * kblocks + kb]) << (8 * g);
+    }
+    packed[w] = v;
+  }
+}
+
 }  // namespace hkmoe

@@ -413,6 +413,57 @@ void dispatch_quant_tensor(py::object x, py::object q, py::object s, py::object 
                            static_cast<float*>(ss.ptr), static_cast<float*>(w.ptr), current_stream()));
 }
 
+// MX (e8m0 1x32) operands: raw exponents are uint8 [R, C/32]; packed
+// exponent words are int32 [C/128, R64] (R64 = R rounded up to 64).
+constexpr const char* kU8 = "torch.uint8";
+
+int64_t round64(int64_t r) { return (r + 63) / 64 * 64; }
+
+void dispatch_quant_mx(py::object x, py::object q, py::object s) {
+  auto xx = as_tensor(x, "x"), qq = as_tensor(q, "q"), ss = as_tensor(s, "s");
+  want_dtype(xx, "x", kF32);
+  want_dtype(qq, "q", kF8);
+  want_dtype(ss, "s", kU8);
+  want_dim(xx, "x", 2);
+  const int64_t r = xx.shape[0], c = xx.shape[1];
+  if (qq.numel() != r * c || ss.numel() != r * (c / 32)) throw std::runtime_error("quant_mx: q [R,C], s [R,C/32]");
+  check(hkmoe_quant_mx(static_cast<const float*>(xx.ptr), r, c, qq.ptr, ss.ptr, current_stream()));
+}
+
+void dispatch_mx_pack_scales(py::object s, int64_t cols, py::object packed) {
+  auto ss = as_tensor(s, "s"), pp = as_tensor(packed, "packed");
+  want_dtype(ss, "s", kU8);
+  want_dtype(pp, "packed", kI32);
+  want_dim(ss, "s", 2);
+  const int64_t r = ss.shape[0];
+  if (cols % 128 != 0 || ss.shape[1] != cols / 32)
+    throw std::runtime_error("mx_pack_scales: s must be [R, cols/32] with cols % 128 == 0");
+  if (pp.numel() != (cols / 128) * round64(r)) throw std::runtime_error("mx_pack_scales: packed must be [cols/128, R64]");
+  check(hkmoe_mx_pack_scales(ss.ptr, r, cols, pp.ptr, current_stream()));
+}
+
+void dispatch_gemm_mx(py::object A, py::object sa, py::object B, py::object sb, py::object C) {
+  auto a = as_tensor(A, "A"), b = as_tensor(B, "B"), c = as_tensor(C, "C");
+  auto as = as_tensor(sa, "scale_a"), bs = as_tensor(sb, "scale_b");
+  want_dtype(a, "A", kF8);
+  want_dtype(b, "B", kF8);
+  want_dtype(as, "scale_a", kI32);
+  want_dtype(bs, "scale_b", kI32);
+  want_dim(a, "A", 2);
+  want_dim(b, "B", 2);
+  want_dim(c, "C", 2);
+  const int64_t m = a.shape[0], k = a.shape[1], n = b.shape[0];
+  if (b.shape[1] != k) throw std::runtime_error("A and B must have the same K");
+  if (c.shape[0] != m || c.shape[1] != n) throw std::runtime_error("C must be [M, N]");
+  if (as.numel() != (k / 128) * round64(m)) throw std::runtime_error("scale_a must be packed [K/128, M64]");
+  if (bs.numel() != (k / 128) * round64(n)) throw std::runtime_error("scale_b must be packed [K/128, N]");
+  int out;
+  if (c.dtype == kBf16) out = HKMOE_BF16;
+  else if (c.dtype == kF32) out = HKMOE_F32;
+  else throw std::runtime_error("C: expected bfloat16 or float32");
+  check(hkmoe_gemm_mx(a.ptr, as.ptr, b.ptr, bs.ptr, c.ptr, m, n, k, out, current_stream()));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(tk_kernel, m) {
@@ -443,6 +494,10 @@ PYBIND11_MODULE(tk_kernel, m) {
   m.def("dispatch_quant_group", &dispatch_quant_group);
   m.def("dispatch_quant_block", &dispatch_quant_block);
   m.def("dispatch_quant_tensor", &dispatch_quant_tensor);
+  m.def("dispatch_quant_mx", &dispatch_quant_mx, "x fp32 [R,C] -> q e4m3 [R,C], e8m0 s uint8 [R,C/32]");
+  m.def("dispatch_mx_pack_scales", &dispatch_mx_pack_scales, py::arg("s"), py::arg("cols"), py::arg("packed"));
+  m.def("dispatch_gemm_mx", &dispatch_gemm_mx, "C = A . B^T with 1x32 e8m0 scales (packed words)",
+        py::arg("A"), py::arg("scale_a"), py::arg("B"), py::arg("scale_b"), py::arg("C"));
   m.def("moe_workspace_size", &moe_workspace_size);
   m.def("route_blocks", [](int64_t t) { return hkmoe_route_blocks(t); });
   m.def("mtile_list_ints", &mtile_list_ints, "ints of an M-tile list for `rows` expert rows over E experts");

@@ -62,6 +62,37 @@ def gemm_fp8(a_q, b_q, scale_a=None, scale_b=None, out_dtype=torch.bfloat16):
 
 
 # ----------------------------------------------------------------------------
+# MX (1x32 e8m0) operands and GEMM
+# ----------------------------------------------------------------------------
+def quant_mx(x):
+    """fp32 [R, C] -> (e4m3 [R, C], e8m0 exponents uint8 [R, C/32])."""
+    _check_dev(x)
+    x = x.float().contiguous()
+    q = torch.empty(x.shape, dtype=F8, device=x.device)
+    s = torch.empty((x.shape[0], x.shape[1] // 32), dtype=torch.uint8, device=x.device)
+    tk_kernel.dispatch_quant_mx(x, q, s)
+    return q, s
+
+
+def mx_pack_scales(s):
+    """e8m0 exponents uint8 [R, C/32] -> packed MFMA words int32 [C/128, R64]."""
+    _check_dev(s)
+    s = s.contiguous()
+    rows, cols = s.shape[0], s.shape[1] * 32
+    packed = torch.empty((cols // 128, (rows + 63) // 64 * 64), dtype=torch.int32, device=s.device)
+    tk_kernel.dispatch_mx_pack_scales(s, cols, packed)
+    return packed
+
+
+def gemm_mx(a_q, a_packed, b_q, b_packed, out_dtype=torch.float32):
+    """C = A . B^T with 1x32 e8m0 block scales (packed by mx_pack_scales)."""
+    _check_dev(a_q, b_q)
+    c = torch.empty((a_q.shape[0], b_q.shape[0]), dtype=out_dtype, device=a_q.device)
+    tk_kernel.dispatch_gemm_mx(a_q, a_packed, b_q, b_packed, c)
+    return c
+
+
+# ----------------------------------------------------------------------------
 # the layer
 # ----------------------------------------------------------------------------
 def pack_weights(w_q, gate_up=False):

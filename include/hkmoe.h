@@ -220,6 +220,45 @@ int hkmoe_quant_block(const float* x, int64_t batch, int64_t rows, int64_t cols,
 int hkmoe_quant_tensor(const float* x, int64_t rows, int64_t cols, void* q, float* s,
                        float* amax_ws, hkmoe_stream_t stream);
 
+/*
+ * MX (microscaling) FP8: e4m3 elements with one e8m0 exponent per row and
+ * 32-element K block.  An e8m0 byte s stands for 2^(s - 127).
+ *
+ * hkmoe_quant_mx: x [R, C] fp32 (finite) -> q [R, C] e4m3, s [R, C/32] e8m0,
+ *   s = clamp(floor(log2(amax32)) + 127, 0, 254) (0 for an all-zero block),
+ *   q = e4m3(x * 2^(127 - s)), round to nearest even.  floor(log2) is exact
+ *   (the biased exponent of amax).  C % 32 == 0.
+ *   Replaces quantize_fp8_kernel and compute_e8m0_scale
+ *   (kernels/cdna4/gemm/mxfp8/MXFP8_4wave/4_wave.cu:296-321, 368-373).
+ */
+int hkmoe_quant_mx(const float* x, int64_t rows, int64_t cols, void* q, void* s,
+                   hkmoe_stream_t stream);
+
+/*
+ * hkmoe_mx_pack_scales: e8m0 s [R, C/32] -> packed [C/128, R64] uint32 words,
+ *   R64 = R rounded up to a multiple of 64, the operand order of the scaled
+ *   MFMA: word (kt, p) holds in byte g the exponent of row 64*(p/64) + 16*g +
+ *   p%16 for K block 4*kt + (p%64)/16 (0 for rows >= R).  C % 128 == 0.
+ *   For R % 64 == 0 the words equal the reference's pack_scales_kernel
+ *   followed by repack_scales_for_mfma_kernel (4_wave.cu:323-364), i.e. the
+ *   words its device-side pack_scales builds
+ *   (include/cdna4/ops/warp/register/tile/mma.cuh:253-270).
+ */
+int hkmoe_mx_pack_scales(const void* s, int64_t rows, int64_t cols, void* packed,
+                         hkmoe_stream_t stream);
+
+/*
+ * hkmoe_gemm_mx: C[M,N] = sum over K blocks kb of
+ *     2^(sa[m,kb] - 127) * 2^(sb[n,kb] - 127) * sum_{k in kb} A[m,k] * B[n,k]
+ *   A [M,K] e4m3 with packed scales a_scale [K/128, M64]; B [N,K] e4m3 with
+ *   packed scales b_scale [K/128, N] (hkmoe_mx_pack_scales); fp32 accumulate,
+ *   C bf16 (RNE) or fp32.  K % 128 == 0, N % 256 == 0, M arbitrary.
+ *   Replaces mxfp8_gemm_4wave_kernel (4_wave.cu:77-292), which is launched
+ *   with the packed scales of prepare_mxfp8_data (4_wave.cu:377-448).
+ */
+int hkmoe_gemm_mx(const void* a, const void* a_scale, const void* b, const void* b_scale, void* c,
+                  int64_t m, int64_t n, int64_t k, int out_dtype, hkmoe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,8 @@ fp8     OCP e4m3fn decode/encode (RNE, saturating) and bf16 RNE, from the bit
         formats.
 spec    quantisers, routing (top-k + softmax), expert offsets, permutation,
         dense/grouped GEMMs, SiLU*up, requantisation, combine, the full layer.
+mx      MX (1x32 e8m0) quantiser, the reference's two-step scale packing,
+        this path's one-step packing, and the MX dequantise-then-matmul GEMM.
 brute   independent per-token brute-force restatement of the layer (no
         permutation, pure Python loops) used to pin ``spec`` on tiny shapes.
 synth   seeded synthetic inputs for every configuration (numpy PCG64).

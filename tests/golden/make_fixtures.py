@@ -14,7 +14,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
 
-from oracle import spec, synth  # noqa: E402
+from oracle import mx, spec, synth  # noqa: E402
 
 OUT = os.path.dirname(os.path.abspath(__file__))
 
@@ -30,6 +30,12 @@ def main():
     c = spec.gemm_fp8(d["a_q"], d["b_q"], d["sa"], d["sb"], out="f32")
     np.savez_compressed(os.path.join(OUT, "dense_m64_n256_k256.npz"), a_q=d["a_q"], b_q=d["b_q"],
                         sa=np.float32(d["sa"]), sb=np.float32(d["sb"]), c_f32=c)
+    # MX: fp32 operands -> e8m0 exponents, e4m3 bytes, packed words, fp32 C
+    d = mx.make_mx_dense(96, 256, 256, seed=24)
+    np.savez_compressed(os.path.join(OUT, "mx_m96_n256_k256.npz"), mx_a=d["a"], mx_b=d["b"], a_q=d["a_q"],
+                        sa=d["sa"], b_q=d["b_q"], sb=d["sb"], sa_packed=mx.mx_pack_scales(d["sa"]),
+                        sb_packed=mx.mx_pack_scales(d["sb"]),
+                        c_f32=mx.gemm_mx(d["a_q"], d["sa"], d["b_q"], d["sb"]))
     for name, cfg in MOE_CASES.items():
         cfg = dict(cfg)
         seed = cfg.pop("seed")

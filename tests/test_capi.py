@@ -120,6 +120,26 @@ def test_pack_weights_argument_errors(lib):
     assert lib.hkmoe_pack_weights(fake, i64(0), i64(512), i64(256), i32(256), other, None) == 0
 
 
+def test_mx_argument_errors(lib):
+    fake = ctypes.c_void_p(0x1000)
+    i64 = ctypes.c_int64
+    assert lib.hkmoe_quant_mx(fake, i64(4), i64(48), fake, fake, None) == 1
+    assert "multiple of 32" in _err(lib)
+    assert lib.hkmoe_quant_mx(None, i64(4), i64(64), fake, fake, None) == 1
+    assert lib.hkmoe_quant_mx(fake, i64(0), i64(64), fake, fake, None) == 0  # empty: no launch
+    assert lib.hkmoe_mx_pack_scales(fake, i64(4), i64(96), fake, None) == 1
+    assert "multiple of 128" in _err(lib)
+    assert lib.hkmoe_gemm_mx(fake, fake, fake, fake, fake, i64(64), i64(256), i64(96), 1, None) == 1
+    assert "multiple of 128" in _err(lib)
+    assert lib.hkmoe_gemm_mx(fake, fake, fake, fake, fake, i64(64), i64(320), i64(128), 1, None) == 1
+    assert "multiple of 256" in _err(lib)
+    assert lib.hkmoe_gemm_mx(fake, None, fake, fake, fake, i64(64), i64(256), i64(128), 1, None) == 1
+    assert "null" in _err(lib)
+    assert lib.hkmoe_gemm_mx(fake, fake, fake, fake, fake, i64(64), i64(256), i64(128), 5, None) == 1
+    assert "out_dtype" in _err(lib)
+    assert lib.hkmoe_gemm_mx(fake, fake, fake, fake, fake, i64(0), i64(256), i64(128), 1, None) == 0
+
+
 def _align(x):
     return (x + 255) // 256 * 256
 

@@ -30,7 +30,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import brute, fp8, spec, synth
+from oracle import brute, fp8, mx, spec, synth
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
@@ -256,6 +256,14 @@ def _golden_cases():
 @pytest.mark.parametrize("name", _golden_cases())
 def test_golden_fixture(name):
     g = np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+    if "mx_a" in g:
+        for op, raw in (("a", "mx_a"), ("b", "mx_b")):
+            q, s = mx.quant_mx(g[raw])
+            np.testing.assert_array_equal(q, g[op + "_q"])
+            np.testing.assert_array_equal(s, g["s" + op])
+            np.testing.assert_array_equal(mx.mx_pack_scales(s), g["s" + op + "_packed"])
+        np.testing.assert_array_equal(mx.gemm_mx(g["a_q"], g["sa"], g["b_q"], g["sb"]), g["c_f32"])
+        return
     if "a_q" in g:
         c = spec.gemm_fp8(g["a_q"], g["b_q"], g["sa"], g["sb"], out="f32")
         np.testing.assert_array_equal(c, g["c_f32"])
