@@ -11,6 +11,11 @@ top-8, Zipf-skewed routing, 128x128 weight / 1x128 activation block scales).
 Synthetic inputs are drawn on the GPU (torch generator, N(0,1)) and quantised
 by the path's own device quantisers.
 
+``--config dense2048|tp_local|mx8192`` runs one dense GEMM per step instead:
+configs 1 and 4 (per-tensor scales, bf16 out) and the reference MXFP8
+harness's 8192^3 shape with 1x32 e8m0 scales (fp32 out); ``value`` is then that
+GEMM's TFLOP/s.
+
 Extra JSON fields: ``roofline`` (dominant kernel: grouped GEMM 1, timed with
 events on the stream it runs on), ``cpu_baseline`` (the oracle's dequantise +
 fp32 per-expert matmul path on a bounded sample of experts, host cores),
@@ -35,6 +40,14 @@ CONFIGS = {
     "mixtral": dict(T=4096, H=4096, I=14336, E=8, k=2, block=False, skew=False),
     "decode": dict(T=64, H=4096, I=1536, E=128, k=8, block=True, skew=False),
 }
+# Dense single-GEMM workloads: configs 1 and 4 (per-tensor scales, bf16 out) and
+# the reference MXFP8 harness's shape (kernels/cdna4/gemm/mxfp8/MXFP8_4wave/
+# 4_wave.cu:23, 386-388: M = N = K = 8192, N(0, 0.5), 1x32 e8m0, fp32 out).
+DENSE = {
+    "dense2048": dict(M=2048, N=2048, K=2048, mx=False, sigma=1.0, out="bf16"),
+    "tp_local": dict(M=8192, N=8192, K=2048, mx=False, sigma=1.0, out="bf16"),
+    "mx8192": dict(M=8192, N=8192, K=8192, mx=True, sigma=0.5, out="f32"),
+}
 
 
 def parse():
@@ -42,7 +55,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="dsv3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="dsv3", choices=sorted(CONFIGS) + sorted(DENSE))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="time budget of the bounded CPU baseline sample")
@@ -203,14 +216,18 @@ def cpu_baseline(inp, cfg, budget_s):
 # ----------------------------------------------------------------------------
 PROF_TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d {d}/trace -o run -- "
                   "python3 bench.py --config {c} --steps 5 --warmup 2 --no-cpu > {d}/bench.json")
+PROF_TRACE_CMD_DENSE = ("rocprofv3 --kernel-trace --stats --output-format csv -d {d}/trace -o run -- "
+                        "python3 bench.py --config {c} --steps 40 --warmup 5 --no-cpu > {d}/bench.json")
 PROF_PMC_CMD = ("rocprofv3 --pmc {ctr} --output-format csv -d {d}/{ctr} -o run -- "
                 "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu --calibrate-copy")
 CALIB_BYTES = 1 << 30
 
 
-def _kernel_label(name):
+def _kernel_label(name, dense=False):
     """Short label of a kernel of this library (None for other kernels)."""
     if "gemm_fp8_persistent" in name:
+        if dense:
+            return "gemm"
         epi = name.split("Epi)")[1][0] if "Epi)" in name else "?"
         return "grouped_gemm1" if epi in "23" else "grouped_gemm2"
     n = name[len("void "):] if name.startswith("void ") else name  # template kernels
@@ -222,6 +239,10 @@ def _kernel_label(name):
 def _algorithmic_bytes(cfg, active):
     """Compulsory HBM bytes per launch (inputs read once, outputs written once;
     weights of the `active` experts only)."""
+    if "M" in cfg:  # dense GEMM: A, B, their scales, C
+        M, N, K = cfg["M"], cfg["N"], cfg["K"]
+        sc = (M + N) * (K // 32) if cfg["mx"] else 8
+        return {"gemm": M * K + N * K + sc + M * N * (4 if cfg["out"] == "f32" else 2)}
     T, H, I, k = cfg["T"], cfg["H"], cfg["I"], cfg["k"]
     rows = T * k
     sc_x = rows * (H // 128) * 4 if cfg["block"] else 4
@@ -235,7 +256,8 @@ def _algorithmic_bytes(cfg, active):
 def summarize_profile(args):
     import csv
     import collections
-    cfg = CONFIGS[args.config]
+    dense = args.config in DENSE
+    cfg = DENSE[args.config] if dense else CONFIGS[args.config]
     d = args.summarize_profile
     out_dir = os.path.join(ROOT, "profiles")
     os.makedirs(out_dir, exist_ok=True)
@@ -243,25 +265,35 @@ def summarize_profile(args):
     rows = []
     with open(stats) as f:
         for r in csv.DictReader(f):
-            lab = _kernel_label(r["Name"])
+            lab = _kernel_label(r["Name"], dense)
             if lab is None:
                 continue
             rows.append((lab, int(r["Calls"]), float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3,
                          float(r["MaxNs"]) / 1e3, float(r["TotalDurationNs"]) / 1e6))
     tot = sum(r[5] for r in rows)
-    name = f"moe_layer_{args.config}"
+    name = f"gemm_{args.config}" if dense else f"moe_layer_{args.config}"
+    what = "dense GEMM" if dense else "MoE layer"
     with open(os.path.join(out_dir, f"{name}_kernels.md"), "w") as f:
-        f.write(f"# rocprofv3 kernel trace: MoE layer, workload `{args.config}`\n\n")
+        f.write(f"# rocprofv3 kernel trace: {what}, workload `{args.config}`\n\n")
         f.write(f"Config: {json.dumps(cfg)}\n\n")
         with open(os.path.join(d, "bench.json")) as bj:
             b = json.loads([ln for ln in bj if ln.startswith("{")][-1])
-        f.write(f"bench line of the traced run: value {b['value']} {b['unit']}, "
-                f"{b['ms_per_step']} ms/step, weights {b['config'].get('weights')}, "
-                f"active experts {b['config']['active_experts']}, event-timed kernels (ms): "
-                f"{json.dumps(b['kernels_ms'])}\n\n")
-        f.write("Command (repo root; bench.py runs warmup + timed steps + a 10-iteration "
-                "per-kernel pass, so call counts include all of them):\n\n")
-        f.write("    " + PROF_TRACE_CMD.format(d="<out>", c=args.config) + "\n\n")
+        if dense:
+            f.write(f"bench line of the traced run: value {b['value']} {b['unit']}, "
+                    f"{b['ms_per_step']} ms/step, event-timed kernel average "
+                    f"{b['roofline']['avg_ms']} ms\n\n")
+        else:
+            f.write(f"bench line of the traced run: value {b['value']} {b['unit']}, "
+                    f"{b['ms_per_step']} ms/step, weights {b['config'].get('weights')}, "
+                    f"active experts {b['config']['active_experts']}, event-timed kernels (ms): "
+                    f"{json.dumps(b['kernels_ms'])}\n\n")
+        if dense:
+            f.write("Command (repo root; the GEMM's call count includes the warmup calls):\n\n")
+            f.write("    " + PROF_TRACE_CMD_DENSE.format(d="<out>", c=args.config) + "\n\n")
+        else:
+            f.write("Command (repo root; bench.py runs warmup + timed steps + a 10-iteration "
+                    "per-kernel pass, so call counts include all of them):\n\n")
+            f.write("    " + PROF_TRACE_CMD.format(d="<out>", c=args.config) + "\n\n")
         f.write("| kernel | calls | avg us | min us | max us | share of library time |\n|---|---|---|---|---|---|\n")
         for lab, n, avg, mn, mx, t in sorted(rows, key=lambda r: -r[5]):
             f.write(f"| {lab} | {n} | {avg:.1f} | {mn:.1f} | {mx:.1f} | {100 * t / tot:.1f}% |\n")
@@ -278,7 +310,7 @@ def summarize_profile(args):
                     continue
                 if r["Kernel_Name"] == "__amd_rocclr_copyBuffer":
                     copies[r["Dispatch_Id"]] += float(r["Counter_Value"])
-                lab = _kernel_label(r["Kernel_Name"])
+                lab = _kernel_label(r["Kernel_Name"], dense)
                 if lab is not None:
                     agg[lab][r["Dispatch_Id"]] += float(r["Counter_Value"])
         big = max(copies.values())  # the 1 GiB calibration copy is the largest copy
@@ -288,11 +320,11 @@ def summarize_profile(args):
     with open(os.path.join(d, "bench.json")) as f:
         line = [ln for ln in f if ln.startswith("{")][-1]
     bench = json.loads(line)
-    active = bench["config"]["active_experts"]
+    active = bench["config"].get("active_experts", 1)
     algo = _algorithmic_bytes(cfg, active)
     traffic = {}
     with open(os.path.join(out_dir, f"{name}_traffic.md"), "w") as f:
-        f.write(f"# HBM traffic per launch: MoE layer, workload `{args.config}`\n\n")
+        f.write(f"# HBM traffic per launch: {what}, workload `{args.config}`\n\n")
         f.write("Two counter passes, one counter each (repo root):\n\n")
         for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
             f.write("    " + PROF_PMC_CMD.format(d="<out>", ctr=ctr, c=args.config) + "\n")
@@ -312,9 +344,12 @@ def summarize_profile(args):
             a = algo.get(lab)
             f.write(f"| {lab} | {fe:,.0f} | {wr:,.0f} | {rd_b / 1e9:.3f} | {wr_b / 1e9:.3f} | "
                     + (f"{a / 1e9:.3f} | {(rd_b + wr_b) / a:.2f} |\n" if a else "- | - |\n"))
-        f.write(f"\nAlgorithmic bytes: operands read once, outputs written once, weights of the "
-                f"{active} active experts only (activations e4m3, intermediates e4m3 + fp32 group "
-                f"scales, y and out bf16).\n")
+        if dense:
+            f.write("\nAlgorithmic bytes: A and B (e4m3) and their scales read once, C written once.\n")
+        else:
+            f.write(f"\nAlgorithmic bytes: operands read once, outputs written once, weights of the "
+                    f"{active} active experts only (activations e4m3, intermediates e4m3 + fp32 group "
+                    f"scales, y and out bf16).\n")
     tj = os.path.join(out_dir, "traffic.json")
     old = {}
     if os.path.exists(tj):
@@ -327,6 +362,113 @@ def summarize_profile(args):
                       "traffic": traffic}))
 
 
+def dense_cpu_baseline(a_q, sa, b_q, sb, cfg, budget_s):
+    """Oracle dequantisation + numpy fp32 matmul of a bounded sample of A rows
+    against the whole of B, timed on the host."""
+    import numpy as np
+    import torch
+    from oracle import mx, spec
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    aq = a_q.view(torch.uint8).cpu().numpy()
+    bq = b_q.view(torch.uint8).cpu().numpy()
+    if cfg["mx"]:
+        san, sbn = sa.cpu().numpy(), sb.cpu().numpy()
+        deq_a = lambda r0, r1: mx.dequant_mx(aq[r0:r1], san[r0:r1]).astype(np.float32)
+        b = mx.dequant_mx(bq, sbn).astype(np.float32)
+    else:
+        sav, sbv = float(sa.cpu()[0]), float(sb.cpu()[0])
+        deq_a = lambda r0, r1: spec.dequant_per_tensor(aq[r0:r1], sav)
+        b = spec.dequant_per_tensor(bq, sbv)
+    bt = np.ascontiguousarray(b.T)
+    rows, elapsed, chunk = 0, 0.0, 64
+    while elapsed < budget_s and rows < cfg["M"]:
+        r1 = min(cfg["M"], rows + chunk)
+        t0 = time.perf_counter()
+        _ = deq_a(rows, r1) @ bt
+        elapsed += time.perf_counter() - t0
+        rows = r1
+    flops = 2.0 * rows * cfg["N"] * cfg["K"]
+    return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "sample": f"{rows} of {cfg['M']} rows of A against all of B: oracle dequantisation "
+                      f"({'1x32 e8m0' if cfg['mx'] else 'per-tensor'}) + numpy fp32 matmul, {elapsed:.1f} s"}
+
+
+def dense_main(args):
+    """One step = one dense GEMM launch on resident operands."""
+    import torch
+    import hkmoe
+    import tk_kernel
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = DENSE[args.config]
+    M, N, K = cfg["M"], cfg["N"], cfg["K"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    a = torch.randn((M, K), generator=g, device=dev) * cfg["sigma"]
+    b = torch.randn((N, K), generator=g, device=dev) * cfg["sigma"]
+    if cfg["mx"]:
+        a_q, sa = hkmoe.quant_mx(a)
+        b_q, sb = hkmoe.quant_mx(b)
+        pa, pb = hkmoe.mx_pack_scales(sa), hkmoe.mx_pack_scales(sb)
+    else:
+        a_q, sa = hkmoe.quant_tensor(a)
+        b_q, sb = hkmoe.quant_tensor(b)
+    del a, b
+    c = torch.empty((M, N), dtype=torch.float32 if cfg["out"] == "f32" else torch.bfloat16, device=dev)
+    if cfg["mx"]:
+        step = lambda: tk_kernel.dispatch_gemm_mx(a_q, pa, b_q, pb, c)
+    else:
+        step = lambda: tk_kernel.dispatch_gemm_fp8(a_q, b_q, c, sa, sb)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    kern_ms = e0.elapsed_time(e1) / args.steps  # one kernel per step, back to back on this stream
+    flops = 2.0 * M * N * K
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    traffic = None
+    if os.path.exists(args.traffic):
+        try:
+            with open(args.traffic) as f:
+                traffic = json.load(f).get(f"{args.config}:gemm")
+        except Exception:
+            traffic = None
+    value = flops / dt / 1e12
+    ach = flops / (kern_ms * 1e-3) / 1e12
+    res = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "e4m3",
+        "data": "synthetic (seeded torch normal on device, quantised by the path's quantisers)",
+        "config": {"workload": f"{args.config}_gemm", "M": M, "N": N, "K": K,
+                   "scales": "1x32 e8m0 (MX)" if cfg["mx"] else "per-tensor", "out": cfg["out"]},
+        "pct_fp8_peak": round(100.0 * value / PEAK_FP8_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "kernel": "gemm_mx" if cfg["mx"] else "gemm_fp8",
+                     "achieved": round(ach, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ach / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
+                     "avg_ms": round(kern_ms, 4), "flops_per_launch": flops},
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = dense_cpu_baseline(a_q, sa, b_q, sb, cfg, min(args.cpu_seconds, 10.0))
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
     if args.summarize_profile:
@@ -336,6 +478,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only: run with --gpus 1 "
                                    "(multi-GPU sharding is a design note, not a measured path)"}))
         sys.exit(2)
+    if args.config in DENSE:
+        dense_main(args)
+        return
     import torch
     import hkmoe
     dev = torch.device("cuda:0")

@@ -40,9 +40,10 @@
 //    (fragments are read in the instruction's K order, read_frag_mx).  The
 //    scales arrive pre-packed so that word (k step kt, position p) of a 64-row
 //    group holds, in byte g, the exponent of row 16g + p%16 of the group for K
-//    block 4kt + (p%64)/16 (mx_pack_scales_kernel); a wave's words for one
-//    64-row group are then 64 consecutive words, DMA'd with the A half (they
-//    add 2 KiB to a stage) and read as one dword per lane: no VALU rescale.
+//    block 4kt + (p%64)/16 (mx_pack_scales_kernel).  A tile's words of one K
+//    step are then 1 KiB contiguous per operand, DMA'd by two instructions with
+//    group 0's A half (2 KiB more per stage), and a lane reads one dword per
+//    64-row group: no VALU rescale.
 //  * optional row gather: A row of output row p is a_gather[p] / gather_div
 //    (the expert-sorted permutation), so GEMM 1 reads token rows in place.
 //  * MFMA operands are swapped (B fragment as src0) so each lane owns 4
@@ -350,23 +351,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       const int ar = p.a_gather ? p.a_gather[rr] / p.gather_div : rr;
       as_voff = static_cast<int>(ar * p.as_rs) * 4;
     }
-    // MX: every wave DMAs one 64-word group per step -- waves 0-1 of a group
-    // the A words of its half, waves 2-3 the B words of rows 128*grp .. +127.
-    // Words past the packed arrays read as zero (rows that are never stored).
+    // MX: a tile's exponent words of one K step are 1 KiB contiguous per
+    // operand, so wave 0 DMAs all 256 A words and wave 1 all 256 B words (one
+    // 16-byte-per-lane instruction each), with group 0's A half.  Group 1 last
+    // read that stage's words three phases earlier (its first memory phase of
+    // the step before).  Words past the packed arrays read as zero (rows that
+    // are never stored).
+    const bool mx_loader = kMX && wave < 2;
     i32x4 mx_srd;
     int mx_voff = 0, mx_kstride = 0, mx_lds = 0;
     if constexpr (kMX) {
       const int k_steps_ = p.K / kBK;
-      if (wg < 2) {
+      if (wave == 0) {
         mx_srd = make_srd(p.a_scale, static_cast<uint32_t>(k_steps_ * p.as_rs * 4));
-        mx_voff = (row0 + wave_row0 + wg * 64 + lane) * 4;
+        mx_voff = (row0 + lane * 4) * 4;
         mx_kstride = static_cast<int>(p.as_rs) * 4;
-        mx_lds = 2 * kTileBytes + (wave_row0 + wg * 64) * 4;
+        mx_lds = 2 * kTileBytes;
       } else {
         mx_srd = make_srd(p.b_scale, static_cast<uint32_t>(k_steps_ * p.nb * 4));
-        mx_voff = (nt * kBN + grp * 128 + (wg - 2) * 64 + lane) * 4;
+        mx_voff = (nt * kBN + lane * 4) * 4;
         mx_kstride = p.nb * 4;
-        mx_lds = 2 * kTileBytes + kScaleBytes + (grp * 128 + (wg - 2) * 64) * 4;
+        mx_lds = 2 * kTileBytes + kScaleBytes;
       }
     }
 
@@ -388,7 +393,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         load_lds_4B(as_srd, sa + 2 * kTileBytes + (wave_row0 + wg * 64) * 4, as_voff,
                     static_cast<int>(kt * p.as_ks) * 4);
       }
-      if constexpr (kMX) load_lds_4B(mx_srd, sa + mx_lds, mx_voff, kt * mx_kstride);
+      if (mx_loader) load_lds_16B(mx_srd, sa + mx_lds, mx_voff, kt * mx_kstride);
     };
     auto issue_b = [&](int kt) {
       uint8_t* sb = smem + (kt & 1) * kStg + kTileBytes;
