@@ -180,25 +180,30 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
     }
   }
   if (mtile_list != nullptr) {
-    // M-tile list [(expert, first row)]: every expert's full tiles first (in
-    // expert order), then the partial tiles.  Tiles of equal cost then sit
-    // together in the grouped GEMMs' schedule, so the workgroups that share a
-    // tile block stay in step and reuse its operands in L2.
+    // M-tile list [(expert, first row)]: first the experts with at least one
+    // full tile, each with all its tiles (full ones, then its partial one),
+    // in expert order; then the single partial tiles of the smaller experts.
+    // Tiles of nearly equal cost sit together in the grouped GEMMs' schedule,
+    // so the workgroups that share a tile block stay in step and reuse its
+    // operands in L2, and a large expert's partial tile runs while its
+    // weights are still in L2 / MALL instead of streaming them once more.
     const int q_full = cnt / tile_m;
     const int q_part = (cnt % tile_m) ? 1 : 0;
-    const int full_base = block_exclusive_scan(q_full, wave_tot);
-    const int part_base = block_exclusive_scan(q_part, wave_tot);
-    __shared__ int n_full;
-    if (part == 0 && e == num_experts - 1) n_full = full_base + q_full;
+    const int q_head = q_full > 0 ? q_full + q_part : 0;
+    const int q_tail = q_full > 0 ? 0 : q_part;
+    const int head_base = block_exclusive_scan(q_head, wave_tot);
+    const int tail_base = block_exclusive_scan(q_tail, wave_tot);
+    __shared__ int n_head;
+    if (part == 0 && e == num_experts - 1) n_head = head_base + q_head;
     __syncthreads();
     if (part == 0 && e < num_experts) {
-      for (int s = 0; s < q_full; ++s) {
-        mtile_list[2 * (full_base + s)] = e;
-        mtile_list[2 * (full_base + s) + 1] = off + s * tile_m;
+      for (int s = 0; s < q_head; ++s) {
+        mtile_list[2 * (head_base + s)] = e;
+        mtile_list[2 * (head_base + s) + 1] = off + s * tile_m;
       }
-      if (q_part) {
-        mtile_list[2 * (n_full + part_base)] = e;
-        mtile_list[2 * (n_full + part_base) + 1] = off + q_full * tile_m;
+      if (q_tail) {
+        mtile_list[2 * (n_head + tail_base)] = e;
+        mtile_list[2 * (n_head + tail_base) + 1] = off;
       }
     }
   }

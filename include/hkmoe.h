@@ -93,8 +93,9 @@ int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_expert
  *   M-tile list), and zeroes *amax_reset and the HKMOE_TILE_COUNTERS ints at
  *   tile_counters when they are non-NULL.
  *   mtile_list (may be NULL): [ceil(T*k/256) + E][2] int32; receives one
- *   (expert, first row) pair per M tile, every expert's full 256-row tiles
- *   first (expert order), then the partial tiles.  Passed to the grouped
+ *   (expert, first row) pair per M tile: first every expert with at least one
+ *   full 256-row tile, with all its tiles (expert order), then the single
+ *   partial tiles of the smaller experts.  Passed to the grouped
  *   GEMMs it sets their tile order (tiles of equal cost run together, which
  *   keeps L2 reuse up); NULL there means expert order.
  */
