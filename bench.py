@@ -39,6 +39,9 @@ CONFIGS = {
     "dsv3": dict(T=8192, H=7168, I=2048, E=256, k=8, block=True, skew=True),
     "mixtral": dict(T=4096, H=4096, I=14336, E=8, k=2, block=False, skew=False),
     "decode": dict(T=64, H=4096, I=1536, E=128, k=8, block=True, skew=False),
+    # config 3's shapes and routing with MX operands (1x32 e8m0 exponents applied
+    # inside the MFMA) instead of fp32 block scales
+    "dsv3_mx": dict(T=8192, H=7168, I=2048, E=256, k=8, block=False, skew=True, mx=True),
 }
 # Dense single-GEMM workloads: configs 1 and 4 (per-tensor scales, bf16 out) and
 # the reference MXFP8 harness's shape (kernels/cdna4/gemm/mxfp8/MXFP8_4wave/
@@ -84,6 +87,25 @@ def make_inputs(cfg, seed, dev):
         rank = torch.randperm(E, generator=g, device=dev).float() + 1.0
         logits += (-1.1 * torch.log(rank))[None, :]
     F8 = torch.float8_e4m3fn
+    if cfg.get("mx"):
+        x_q, x_e = hkmoe.quant_mx(x)
+        del x
+        w13_q = torch.empty((E, 2 * I, H), dtype=F8, device=dev)
+        w2_q = torch.empty((E, H, I), dtype=F8, device=dev)
+        w13_e = torch.empty((E, 2 * I, H // 32), dtype=torch.uint8, device=dev)
+        w2_e = torch.empty((E, H, I // 32), dtype=torch.uint8, device=dev)
+        chunk = max(1, int(2e9 // (2 * I * H * 4)))
+        for e0 in range(0, E, chunk):
+            e1 = min(E, e0 + chunk)
+            for wq, we, shape in ((w13_q, w13_e, (2 * I, H)), (w2_q, w2_e, (H, I))):
+                w = torch.randn(((e1 - e0) * shape[0], shape[1]), generator=g, device=dev, dtype=torch.float32)
+                q, s = hkmoe.quant_mx(w)
+                wq[e0:e1].copy_(q.view(e1 - e0, *shape))
+                we[e0:e1].copy_(s.view(e1 - e0, shape[0], shape[1] // 32))
+                del w, q, s
+        torch.cuda.synchronize()
+        return dict(x_q=x_q, x_scale=x_e, logits=logits, w13_q=w13_q, w13_scale=w13_e, w2_q=w2_q,
+                    w2_scale=w2_e, top_k=k)
     w13_q = torch.empty((E, 2 * I, H), dtype=F8, device=dev)
     w2_q = torch.empty((E, H, I), dtype=F8, device=dev)
     if cfg["block"]:
@@ -120,12 +142,50 @@ def gemm_flops(cfg):
     return 2.0 * rows * (2 * cfg["I"]) * cfg["H"] + 2.0 * rows * cfg["H"] * cfg["I"]
 
 
+def kernel_breakdown_mx(inp, layer, iters=10):
+    """kernel_breakdown for the MX layer (its own GEMM entry points and the
+    activation-exponent gather)."""
+    import torch
+    import tk_kernel
+    import hkmoe
+    pk = layer.packed
+    r = hkmoe.moe_forward_mx_steps(inp["x_q"], inp["x_scale"], inp["logits"], layer.w13_q, layer.w13_words,
+                                   layer.w2_q, layer.w2_words, inp["top_k"], packed=pk)
+    T = inp["x_q"].shape[0]
+    k = inp["top_k"]
+    rows = T * k
+    calls = [
+        ("route_topk", lambda: tk_kernel.dispatch_route_topk(inp["logits"], r["topk_idx"], r["topk_w"], r["block_counts"])),
+        ("expert_offsets", lambda: tk_kernel.dispatch_expert_offsets(r["block_counts"], T, r["counts"], r["offsets"], r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"], r["mtile_list"])),
+        ("scatter", lambda: tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"], r["inv_perm"], None, None, None, None)),
+        ("mx_gather_words", lambda: tk_kernel.dispatch_mx_gather_scales(inp["x_scale"], r["perm"], k, r["offsets"], r["mtile_offsets"], rows, r["xw"])),
+        ("grouped_gemm1", lambda: tk_kernel.dispatch_grouped_gemm1_mx(inp["x_q"], r["xw"], r["perm"], k, layer.w13_q, layer.w13_words, r["offsets"], r["mtile_offsets"], r["hq"], r["hw"], r["tile_ctr"][:8], packed=pk, mtile_list=r["mtile_list"])),
+        ("grouped_gemm2", lambda: tk_kernel.dispatch_grouped_gemm2_mx(r["hq"], r["hw"], layer.w2_q, layer.w2_words, r["offsets"], r["mtile_offsets"], r["y"], r["tile_ctr"][8:], packed=pk, mtile_list=r["mtile_list"])),
+        ("combine", lambda: tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])),
+    ]
+    ev = {name: [] for name, _ in calls}
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        for name, fn in calls:
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            ev[name].append((s, e))
+    torch.cuda.synchronize()
+    ms = {name: sum(s.elapsed_time(e) for s, e in lst) / len(lst) for name, lst in ev.items()}
+    return ms, r
+
+
 def kernel_breakdown(inp, layer, iters=10):
     """Average ms of each kernel of the stepwise layer, events on torch's current
     stream (the stream every dispatch_* call launches on)."""
     import torch
     import tk_kernel
     import hkmoe
+    if hasattr(layer, "w13_words"):
+        return kernel_breakdown_mx(inp, layer, iters)
     pk = layer.packed
     w13, w2 = layer.w13_q, layer.w2_q
     r = hkmoe.moe_forward_steps(inp["x_q"], inp["x_scale"], inp["logits"], w13,
@@ -179,7 +239,8 @@ def cpu_baseline(inp, cfg, budget_s):
     x_q = inp["x_q"].view(__import__("torch").uint8).cpu().numpy()
     xs = inp["x_scale"].cpu().numpy()
     block = cfg["block"]
-    xs = xs if block else np.float32(xs.reshape(-1)[0])
+    is_mx = bool(cfg.get("mx"))
+    xs = xs if (block or is_mx) else np.float32(xs.reshape(-1)[0])
     order = np.argsort(-counts, kind="stable")
     flops = 0.0
     experts = []
@@ -195,11 +256,19 @@ def cpu_baseline(inp, cfg, budget_s):
         s13 = inp["w13_scale"][e].cpu().numpy()
         s2 = inp["w2_scale"][e].cpu().numpy()
         t0 = time.perf_counter()
-        xa = spec.dequant_act(x_q[tok], xs[tok] if block else xs)
-        z = xa @ spec.dequant_weight(w13, s13).T
-        h = spec.bf16_round(spec.silu_mul(z[:, :cfg["I"]], z[:, cfg["I"]:]))
-        hq, hs = spec.requant(h, block)
-        _ = spec.bf16_round(spec.dequant_act(hq, hs) @ spec.dequant_weight(w2, s2).T)
+        if is_mx:
+            from oracle import mx
+            xa = mx.dequant_mx(x_q[tok], xs[tok]).astype(np.float32)
+            z = xa @ mx.dequant_mx(w13, s13).astype(np.float32).T
+            h = spec.bf16_round(spec.silu_mul(z[:, :cfg["I"]], z[:, cfg["I"]:]))
+            hq, hs = mx.quant_mx(h)
+            _ = spec.bf16_round(mx.dequant_mx(hq, hs).astype(np.float32) @ mx.dequant_mx(w2, s2).astype(np.float32).T)
+        else:
+            xa = spec.dequant_act(x_q[tok], xs[tok] if block else xs)
+            z = xa @ spec.dequant_weight(w13, s13).T
+            h = spec.bf16_round(spec.silu_mul(z[:, :cfg["I"]], z[:, cfg["I"]:]))
+            hq, hs = spec.requant(h, block)
+            _ = spec.bf16_round(spec.dequant_act(hq, hs) @ spec.dequant_weight(w2, s2).T)
         elapsed += time.perf_counter() - t0
         flops += 2.0 * (hi - lo) * 3 * cfg["I"] * cfg["H"]
         experts.append(int(e))
@@ -207,7 +276,8 @@ def cpu_baseline(inp, cfg, budget_s):
     return {"value": flops / elapsed / 1e12 if elapsed > 0 else None, "unit": "TFLOP/s",
             "cores": int(threads), "kind": "port",
             "sample": f"{len(experts)} of {int((counts > 0).sum())} active experts (heaviest first, "
-                      f"{int(sum(counts[e] for e in experts))} rows), numpy fp32 dequantise + matmul, "
+                      f"{int(sum(counts[e] for e in experts))} rows), numpy fp32 dequantise "
+                      f"({'1x32 e8m0' if is_mx else 'fp32 scales'}) + matmul, "
                       f"{elapsed:.1f} s"}
 
 
@@ -229,7 +299,7 @@ def _kernel_label(name, dense=False):
         if dense:
             return "gemm"
         epi = name.split("Epi)")[1][0] if "Epi)" in name else "?"
-        return "grouped_gemm1" if epi in "23" else "grouped_gemm2"
+        return "grouped_gemm1" if epi in "234" else "grouped_gemm2"
     n = name[len("void "):] if name.startswith("void ") else name  # template kernels
     if n.startswith("hkmoe::"):
         return n[len("hkmoe::"):].split("(")[0].split("<")[0].replace("_kernel", "")
@@ -245,10 +315,15 @@ def _algorithmic_bytes(cfg, active):
         return {"gemm": M * K + N * K + sc + M * N * (4 if cfg["out"] == "f32" else 2)}
     T, H, I, k = cfg["T"], cfg["H"], cfg["I"], cfg["k"]
     rows = T * k
-    sc_x = rows * (H // 128) * 4 if cfg["block"] else 4
-    sc_h = rows * (I // 128) * 4 if cfg["block"] else 4
-    g1 = active * 2 * I * H + T * H + sc_x + rows * I + sc_h
-    g2 = active * H * I + rows * I + sc_h + rows * H * 2
+    if cfg.get("mx"):  # one e8m0 byte per 32 elements (packed 4 per word)
+        sc_x, sc_h = rows * (H // 32), rows * (I // 32)
+        sw1, sw2 = active * 2 * I * (H // 32), active * H * (I // 32)
+    else:
+        sc_x = rows * (H // 128) * 4 if cfg["block"] else 4
+        sc_h = rows * (I // 128) * 4 if cfg["block"] else 4
+        sw1 = sw2 = 0
+    g1 = active * 2 * I * H + sw1 + T * H + sc_x + rows * I + sc_h
+    g2 = active * H * I + sw2 + rows * I + sc_h + rows * H * 2
     comb = rows * H * 2 + T * H * 2 + rows * 8
     return {"grouped_gemm1": g1, "grouped_gemm2": g2, "combine": comb}
 
@@ -487,8 +562,12 @@ def main():
     torch.cuda.set_device(dev)
     cfg = CONFIGS[args.config]
     inp = make_inputs(cfg, args.seed, dev)
-    layer = hkmoe.MoELayer(inp["w13_q"], inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"],
-                           pack=args.weights == "packed")
+    if cfg.get("mx"):
+        layer = hkmoe.MoELayerMX(inp["w13_q"], inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"],
+                                 pack=args.weights == "packed")
+    else:
+        layer = hkmoe.MoELayer(inp["w13_q"], inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"],
+                               pack=args.weights == "packed")
     out = torch.empty((cfg["T"], cfg["H"]), dtype=torch.bfloat16, device=dev)
     for _ in range(args.warmup):
         layer(inp["x_q"], inp["x_scale"], inp["logits"], out=out)
@@ -526,7 +605,8 @@ def main():
         "data": "synthetic (seeded torch N(0,1) on device, quantised by the path's quantisers)",
         "config": {"workload": f"{args.config}_moe_layer", "T": cfg["T"], "hidden": cfg["H"],
                    "inter": cfg["I"], "experts": cfg["E"], "top_k": cfg["k"],
-                   "scales": "128x128 weight / 1x128 activation blocks" if cfg["block"] else "per-tensor",
+                   "scales": ("1x32 e8m0 (MX) weights and activations" if cfg.get("mx") else
+                              "128x128 weight / 1x128 activation blocks" if cfg["block"] else "per-tensor"),
                    "routing": "zipf(1.1) skew" if cfg["skew"] else "N(0,1) logits",
                    "weights": args.weights,
                    "active_experts": int((counts > 0).sum()), "max_rows": int(counts.max())},

@@ -381,13 +381,19 @@ struct MoeWorkspace {
   int32_t* inv_perm;
   uint16_t* h;   // per-tensor mode only: bf16 intermediate before requantisation
   uint8_t* hq;
-  float* hs;
+  float* hs;     // block: group scales; MX: packed e8m0 words of hq [I/128][ws]
+  uint32_t* xw;  // MX only: packed e8m0 words of the gathered x rows [H/128][ws]
   uint16_t* y;
   size_t bytes;
 };
 
+// Words per K step of the tile-aligned MX exponent layouts: every M tile
+// (at most ceil(rows/256) + E of them) owns 256 words.
+int64_t mx_words_per_step(int64_t rows, int32_t e) { return ((rows + kBM - 1) / kBM + e) * kBM; }
+
 MoeWorkspace carve(uint8_t* base, int64_t t, int32_t e, int32_t k, int32_t hidden, int32_t inter,
-                   bool block) {
+                   int mode) {
+  const bool block = mode == HKMOE_SCALE_BLOCK, mx = mode == HKMOE_SCALE_MX;
   MoeWorkspace w{};
   size_t off = 0;
   const int64_t r = t * k;
@@ -409,9 +415,11 @@ MoeWorkspace carve(uint8_t* base, int64_t t, int32_t e, int32_t k, int32_t hidde
   w.tile_ctr = reinterpret_cast<int32_t*>(take(HKMOE_TILE_COUNTERS * 4));
   w.perm = reinterpret_cast<int32_t*>(take(r * 4));
   w.inv_perm = reinterpret_cast<int32_t*>(take(r * 4));
-  w.h = block ? nullptr : reinterpret_cast<uint16_t*>(take(r * inter * 2));
+  const int64_t ws = mx_words_per_step(r, e);
+  w.h = (block || mx) ? nullptr : reinterpret_cast<uint16_t*>(take(r * inter * 2));
   w.hq = take(r * inter);
-  w.hs = reinterpret_cast<float*>(take(block ? r * (inter / kGroup) * 4 : 4));
+  w.hs = reinterpret_cast<float*>(take(block ? r * (inter / kGroup) * 4 : mx ? (inter / kGroup) * ws * 4 : 4));
+  w.xw = mx ? reinterpret_cast<uint32_t*>(take((hidden / kGroup) * ws * 4)) : nullptr;
   w.y = reinterpret_cast<uint16_t*>(take(r * hidden * 2));
   w.bytes = off;
   return w;
@@ -421,8 +429,9 @@ MoeWorkspace carve(uint8_t* base, int64_t t, int32_t e, int32_t k, int32_t hidde
 size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k,
                                 int32_t hidden, int32_t inter, int scale_mode) {
   if (num_tokens < 0 || num_experts < 1 || top_k < 1 || hidden < 1 || inter < 1) return 0;
-  return carve(nullptr, num_tokens, num_experts, top_k, hidden, inter,
-               scale_mode == HKMOE_SCALE_BLOCK).bytes;
+  if (scale_mode != HKMOE_SCALE_TENSOR && scale_mode != HKMOE_SCALE_BLOCK && scale_mode != HKMOE_SCALE_MX)
+    return 0;
+  return carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, scale_mode).bytes;
 }
 
 int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
@@ -444,14 +453,14 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
              "moe_forward: hidden=%d must be a multiple of 256 and <= %d", hidden, kGroup * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "moe_forward: inter=%d must be a multiple of 128", inter);
   const bool block = scale_mode == HKMOE_SCALE_BLOCK;
-  const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, block);
+  const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, scale_mode);
   if (workspace == nullptr || workspace_bytes < need.bytes)
     return fail(HKMOE_ERR_WORKSPACE, "moe_forward: workspace of %zu bytes needed, %zu given", need.bytes,
                 workspace_bytes);
   HK_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "moe_forward: workspace must be 256-byte aligned");
   if (num_tokens == 0) return HKMOE_OK;
   const MoeWorkspace w = carve(static_cast<uint8_t*>(workspace), num_tokens, num_experts, top_k,
-                               hidden, inter, block);
+                               hidden, inter, scale_mode);
   const int64_t rows = num_tokens * top_k;
   HK_TRY(hkmoe_route_topk(logits, num_tokens, num_experts, top_k, w.topk_idx, w.topk_w,
                           w.block_counts, stream));
@@ -587,4 +596,176 @@ int hkmoe_gemm_mx(const void* a, const void* a_scale, const void* b, const void*
                                  : launch_gemm<Epi::kStoreF32, Scale::kMX>(p, st);
 }
 
+
+int64_t hkmoe_mx_words_per_step(int64_t rows, int32_t num_experts) {
+  return rows < 0 || num_experts < 1 ? 0 : mx_words_per_step(rows, num_experts);
+}
+
+int hkmoe_mx_pack_weight_scales(const void* s, int64_t num_experts, int64_t n, int64_t k, int32_t gate_up,
+                                void* words, hkmoe_stream_t stream) {
+  HK_REQUIRE(s && words, "mx_pack_weight_scales: null pointer");
+  HK_REQUIRE(num_experts >= 0 && n > 0 && k > 0 && n % kBN == 0 && k % kBK == 0,
+             "mx_pack_weight_scales: N=%lld must be a multiple of 256 and K=%lld of 128", (long long)n,
+             (long long)k);
+  HK_REQUIRE(gate_up == 0 || (gate_up > 0 && 2ll * gate_up == n && gate_up % 128 == 0),
+             "mx_pack_weight_scales: gate_up=%d must be 0 or N/2 (a multiple of 128)", gate_up);
+  HK_REQUIRE(k <= (1 << 20), "mx_pack_weight_scales: K too large");
+  const int64_t n_words = num_experts * n * (k / 128);
+  if (n_words == 0) return HKMOE_OK;
+  const int grid = static_cast<int>(std::min<int64_t>((n_words + 255) / 256, 8192));
+  hipLaunchKernelGGL(mx_pack_weight_words_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint8_t*>(s), n, static_cast<int>(k), gate_up,
+                     static_cast<uint32_t*>(words), n_words);
+  return check_launch("mx_pack_weight_words_kernel");
+}
+
+int hkmoe_mx_gather_scales(const void* s, int64_t x_rows, int32_t k, const int32_t* gather, int32_t gather_div,
+                           const int32_t* offsets, const int32_t* mtile_offsets, int32_t num_experts,
+                           int64_t rows, void* words, hkmoe_stream_t stream) {
+  HK_REQUIRE(s && offsets && mtile_offsets && words, "mx_gather_scales: null pointer");
+  HK_REQUIRE(k > 0 && k % kBK == 0, "mx_gather_scales: K=%d must be a multiple of 128", k);
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "mx_gather_scales: bad E=%d", num_experts);
+  HK_REQUIRE(rows >= 0 && rows < (1ll << 31) && x_rows >= 0, "mx_gather_scales: bad rows");
+  HK_REQUIRE(gather != nullptr ? gather_div >= 1 : x_rows >= rows, "mx_gather_scales: bad gather");
+  if (rows == 0) return HKMOE_OK;
+  const int64_t ws = mx_words_per_step(rows, num_experts);
+  const int grid = static_cast<int>(std::min<int64_t>((ws * (k / kBK) + 255) / 256, 8192));
+  hipLaunchKernelGGL(mx_gather_words_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint8_t*>(s), k, gather, gather ? gather_div : 1, offsets, mtile_offsets,
+                     num_experts, ws, static_cast<uint32_t*>(words));
+  return check_launch("mx_gather_words_kernel");
+}
+
+int hkmoe_grouped_gemm1_mx(const void* x, const void* x_words, const int32_t* gather, int32_t gather_div,
+                           int64_t x_rows, const void* w13, const void* w13_words, const int32_t* offsets,
+                           const int32_t* mtile_offsets, const int32_t* mtile_list, int64_t rows,
+                           int32_t num_experts, int32_t hidden, int32_t inter, int w_layout, int out_format,
+                           void* h, void* h_words, int32_t* tile_counters, hkmoe_stream_t stream) {
+  HK_REQUIRE(x && x_words && w13 && w13_words && offsets && mtile_offsets && h, "grouped_gemm1_mx: null pointer");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1_mx: bad E=%d", num_experts);
+  HK_REQUIRE(hidden > 0 && hidden % kGroup == 0 && hidden <= kGroup * kMaxKBlocks,
+             "grouped_gemm1_mx: hidden=%d must be a multiple of 128 and <= %d", hidden, kGroup * kMaxKBlocks);
+  HK_REQUIRE(inter > 0 && inter % 128 == 0, "grouped_gemm1_mx: inter=%d must be a multiple of 128", inter);
+  HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm1_mx: bad rows");
+  HK_REQUIRE(x_rows >= 1 && x_rows * hidden < (1ll << 32), "grouped_gemm1_mx: x_rows=%lld out of range",
+             (long long)x_rows);
+  HK_REQUIRE(gather == nullptr || gather_div >= 1, "grouped_gemm1_mx: gather_div must be >= 1");
+  HK_REQUIRE(gather != nullptr || x_rows >= rows, "grouped_gemm1_mx: x has fewer rows than rows");
+  HK_REQUIRE(2ll * inter * hidden < (1ll << 32), "grouped_gemm1_mx: expert weight too large");
+  HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "grouped_gemm1_mx: bad w_layout %d",
+             w_layout);
+  HK_REQUIRE(out_format == HKMOE_BF16 || out_format == HKMOE_E4M3, "grouped_gemm1_mx: bad out_format %d",
+             out_format);
+  HK_REQUIRE(out_format != HKMOE_E4M3 || h_words != nullptr, "grouped_gemm1_mx: e4m3 output needs h_words");
+  if (rows == 0) return HKMOE_OK;
+  const int64_t ws = mx_words_per_step(rows, num_experts);
+  HK_REQUIRE(ws * (std::max(hidden, inter) / kBK) * 4 < (1ll << 32), "grouped_gemm1_mx: too many rows");
+  GemmParams p{};
+  p.a = static_cast<const uint8_t*>(x);
+  p.a_gather = gather;
+  p.gather_div = gather ? gather_div : 1;
+  p.b = static_cast<const uint8_t*>(w13);
+  p.c = h;
+  p.a_scale = static_cast<const float*>(x_words);
+  p.b_scale = static_cast<const float*>(w13_words);
+  p.c_scale = static_cast<float*>(h_words);
+  p.offsets = offsets;
+  p.mtile_offsets = mtile_offsets;
+  p.rows = rows;
+  p.a_rows = x_rows;
+  p.as_rs = ws;
+  p.cs_rs = ws;
+  p.num_experts = num_experts;
+  p.K = hidden;
+  p.nb = 2 * inter;
+  p.n_out = inter;
+  p.n_tiles = inter / 128;
+  p.b_packed = w_layout == HKMOE_W_PACKED;
+  p.mtile_list = mtile_list;
+  p.blk_m_log2 = 1;  // 2 x 16 tile blocks
+  p.tile_ctr = tile_counters;
+  auto st = static_cast<hipStream_t>(stream);
+  return out_format == HKMOE_E4M3 ? launch_gemm<Epi::kSiluMx, Scale::kMX>(p, st)
+                                  : launch_gemm<Epi::kSiluBf16, Scale::kMX>(p, st);
+}
+
+int hkmoe_grouped_gemm2_mx(const void* hq, const void* hq_words, const void* w2, const void* w2_words,
+                           const int32_t* offsets, const int32_t* mtile_offsets, const int32_t* mtile_list,
+                           int64_t rows, int32_t num_experts, int32_t hidden, int32_t inter, int w_layout,
+                           void* y, int32_t* tile_counters, hkmoe_stream_t stream) {
+  HK_REQUIRE(hq && hq_words && w2 && w2_words && offsets && mtile_offsets && y, "grouped_gemm2_mx: null pointer");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2_mx: bad E=%d", num_experts);
+  HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2_mx: hidden=%d must be a multiple of 256", hidden);
+  HK_REQUIRE(inter > 0 && inter % kGroup == 0 && inter <= kGroup * kMaxKBlocks,
+             "grouped_gemm2_mx: inter=%d must be a multiple of 128 and <= %d", inter, kGroup * kMaxKBlocks);
+  HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm2_mx: bad rows");
+  HK_REQUIRE(static_cast<int64_t>(hidden) * inter < (1ll << 32), "grouped_gemm2_mx: expert weight too large");
+  HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "grouped_gemm2_mx: bad w_layout %d",
+             w_layout);
+  if (rows == 0) return HKMOE_OK;
+  const int64_t ws = mx_words_per_step(rows, num_experts);
+  HK_REQUIRE(ws * (inter / kBK) * 4 < (1ll << 32), "grouped_gemm2_mx: too many rows");
+  GemmParams p{};
+  p.a = static_cast<const uint8_t*>(hq);
+  p.b = static_cast<const uint8_t*>(w2);
+  p.c = y;
+  p.a_scale = static_cast<const float*>(hq_words);
+  p.b_scale = static_cast<const float*>(w2_words);
+  p.offsets = offsets;
+  p.mtile_offsets = mtile_offsets;
+  p.rows = rows;
+  p.a_rows = rows;
+  p.as_rs = ws;
+  p.num_experts = num_experts;
+  p.K = inter;
+  p.nb = hidden;
+  p.n_out = hidden;
+  p.n_tiles = hidden / kBN;
+  p.b_packed = w_layout == HKMOE_W_PACKED;
+  p.mtile_list = mtile_list;
+  p.blk_m_log2 = 1;
+  p.tile_ctr = tile_counters;
+  return launch_gemm<Epi::kStoreBf16, Scale::kMX>(p, static_cast<hipStream_t>(stream));
+}
+
+int hkmoe_moe_forward_mx(const void* x_q, const void* x_e8m0, const float* logits, const void* w13,
+                         const void* w13_words, const void* w2, const void* w2_words, int64_t num_tokens,
+                         int32_t num_experts, int32_t top_k, int32_t hidden, int32_t inter, int w_layout,
+                         void* out, void* workspace, size_t workspace_bytes, hkmoe_stream_t stream) {
+  HK_REQUIRE(x_q && x_e8m0 && logits && w13 && w13_words && w2 && w2_words && out, "moe_forward_mx: null pointer");
+  HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "moe_forward_mx: bad w_layout %d",
+             w_layout);
+  HK_REQUIRE(num_tokens >= 0 && num_tokens * top_k < (1ll << 31), "moe_forward_mx: bad T");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "moe_forward_mx: E=%d outside [1, %d]",
+             num_experts, kMaxExperts);
+  HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK, "moe_forward_mx: bad top_k=%d", top_k);
+  HK_REQUIRE(hidden > 0 && hidden % kBN == 0 && hidden <= kGroup * kMaxKBlocks,
+             "moe_forward_mx: hidden=%d must be a multiple of 256 and <= %d", hidden, kGroup * kMaxKBlocks);
+  HK_REQUIRE(inter > 0 && inter % 128 == 0 && inter <= kGroup * kMaxKBlocks,
+             "moe_forward_mx: inter=%d must be a multiple of 128 and <= %d", inter, kGroup * kMaxKBlocks);
+  const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, HKMOE_SCALE_MX);
+  if (workspace == nullptr || workspace_bytes < need.bytes)
+    return fail(HKMOE_ERR_WORKSPACE, "moe_forward_mx: workspace of %zu bytes needed, %zu given", need.bytes,
+                workspace_bytes);
+  HK_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "moe_forward_mx: workspace must be 256-byte aligned");
+  if (num_tokens == 0) return HKMOE_OK;
+  const MoeWorkspace w = carve(static_cast<uint8_t*>(workspace), num_tokens, num_experts, top_k, hidden,
+                               inter, HKMOE_SCALE_MX);
+  const int64_t rows = num_tokens * top_k;
+  HK_TRY(hkmoe_route_topk(logits, num_tokens, num_experts, top_k, w.topk_idx, w.topk_w, w.block_counts, stream));
+  HK_TRY(hkmoe_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets, w.block_base,
+                              w.mtile_offsets, w.mtile_list, w.amax, w.tile_ctr, stream));
+  HK_TRY(hkmoe_scatter(w.topk_idx, num_tokens, num_experts, top_k, w.offsets, w.block_base, w.perm, w.inv_perm,
+                       nullptr, nullptr, hidden, HKMOE_SCALE_TENSOR, nullptr, nullptr, stream));
+  // token exponents -> tile-aligned words in expert order (x rows stay in place)
+  HK_TRY(hkmoe_mx_gather_scales(x_e8m0, num_tokens, hidden, w.perm, top_k, w.offsets, w.mtile_offsets,
+                                num_experts, rows, w.xw, stream));
+  HK_TRY(hkmoe_grouped_gemm1_mx(x_q, w.xw, w.perm, top_k, num_tokens, w13, w13_words, w.offsets, w.mtile_offsets,
+                                w.mtile_list, rows, num_experts, hidden, inter, w_layout, HKMOE_E4M3, w.hq, w.hs,
+                                w.tile_ctr, stream));
+  HK_TRY(hkmoe_grouped_gemm2_mx(w.hq, w.hs, w2, w2_words, w.offsets, w.mtile_offsets, w.mtile_list, rows,
+                                num_experts, hidden, inter, w_layout, w.y, w.tile_ctr + 8, stream));
+  HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
+  return HKMOE_OK;
+}
 }  // extern "C"

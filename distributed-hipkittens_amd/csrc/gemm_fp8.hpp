@@ -74,19 +74,22 @@
 
 namespace hkmoe {
 
-enum class Epi : int { kStoreBf16 = 0, kStoreF32 = 1, kSiluBf16 = 2, kSiluQuant = 3 };
+enum class Epi : int { kStoreBf16 = 0, kStoreF32 = 1, kSiluBf16 = 2, kSiluQuant = 3, kSiluMx = 4 };
 enum class Scale : int { kTensor = 0, kBlock = 1, kMX = 2 };
 
 struct GemmParams {
   const uint8_t* a;            // A rows [a_rows, K] e4m3
   const int32_t* a_gather;     // optional: A row of output row p = a_gather[p] / gather_div
   const uint8_t* b;            // [E, nb, K] e4m3, row-major or packed (b_packed)
-  void* c;                     // [rows, n_out]: bf16, fp32 or (kSiluQuant) e4m3
+  void* c;                     // [rows, n_out]: bf16, fp32 or (kSiluQuant, kSiluMx) e4m3
   const float* a_scale;        // kTensor: [1] or null (1.0); kBlock: a_scale[r*as_rs + kb*as_ks]
-                               // kMX: packed e8m0 words [K/128][as_rs] (as_rs = rows rounded up to 64)
+                               // kMX: packed e8m0 words [K/128][as_rs]; dense: by row (as_rs =
+                               // rows rounded up to 64); grouped: by M tile m, words m*256 ..
   const float* b_scale;        // kTensor: [E] or null (1.0); kBlock: [E, nb/128, K/128]
-                               // kMX: packed e8m0 words [K/128][nb]
+                               // kMX: packed e8m0 words; dense [K/128][nb]; grouped, per
+                               // B tile: [E][nb/256][K/128][256] (word p = B tile row p)
   float* c_scale;              // kSiluQuant: group scales, transposed [n_out/128, rows]
+                               // kSiluMx: packed e8m0 words of h, [n_out/128][cs_rs] by M tile
   const int32_t* offsets;      // [E+1] row offsets; nullptr = dense (one segment of `rows`)
   const int32_t* mtile_offsets;// [E+1] M-tile offsets; nullptr = dense
   const int32_t* mtile_list;   // optional [M tiles][2] = (expert, first row), in schedule order
@@ -104,6 +107,7 @@ struct GemmParams {
   int32_t n_tiles;             // N tiles per M tile
   int32_t b_packed;            // 1: b is in the packed tile layout of pack_weights_kernel
   int32_t blk_m_log2;          // tile blocks are 2^blk_m_log2 M tiles x 32 / 2^blk_m_log2 N tiles
+  int64_t cs_rs;               // kSiluMx: words per K step of the packed h exponents
 };
 
 constexpr int kBM = 256, kBN = 256, kBK = 128;
@@ -118,6 +122,7 @@ constexpr int kMainLds = 2 * kStageBytes + kBsBytes;
 constexpr int kCtLdStore = kBN + 8;                      // bf16 elements per staged row
 constexpr int kCtLdSilu = 128 + 8;
 constexpr int kEpiLds = kBM * kCtLdStore * 2;
+static_assert(kBM * kCtLdSilu * 2 + kBM * 4 <= kEpiLds, "SiLU staging + MX exponents fit the epilogue LDS");
 constexpr int kLdsData = kMainLds > kEpiLds ? kMainLds : kEpiLds;
 constexpr int kLdsBytes = kLdsData + 16;                 // + the broadcast slot of the tile queue
 constexpr int kGroupM = 8;
@@ -209,10 +214,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 
   constexpr bool kBlockSc = (SC == Scale::kBlock);
   constexpr bool kMX = (SC == Scale::kMX);
-  constexpr bool kSilu = (EPI == Epi::kSiluBf16 || EPI == Epi::kSiluQuant);
+  constexpr bool kSilu = (EPI == Epi::kSiluBf16 || EPI == Epi::kSiluQuant || EPI == Epi::kSiluMx);
   // stage: A tile, B tile, A scales (1 KiB) and, in MX mode, B scales (1 KiB)
   constexpr int kStg = kMX ? kStageBytes + kScaleBytes : kStageBytes;
-  static_assert(!(kMX && kSilu), "MX scales are for the plain-store GEMM");
+  static_assert(EPI != Epi::kSiluMx || kMX, "MX requantisation needs MX scales");
   static_assert(2 * kStg <= kLdsData, "LDS budget");
 
   const int tid = threadIdx.x;
@@ -291,6 +296,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 
     // ---- M tile -> expert segment ----------------------------------------
     int e = 0, row0 = 0, valid = 0;
+    int mnat = mt_glob;  // M tile index in expert order (MX exponent words are by M tile)
     if (dense) {
       row0 = mt_glob * kBM;
       valid = static_cast<int>(min<int64_t>(kBM, p.rows - row0));
@@ -298,6 +304,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       e = p.mtile_list[2 * mt_glob];
       row0 = p.mtile_list[2 * mt_glob + 1];
       valid = min(kBM, p.offsets[e + 1] - row0);
+      mnat = p.mtile_offsets[e] + (row0 - p.offsets[e]) / kBM;
     } else {
       int lo = 0, hi = p.num_experts;  // largest e with mtile_offsets[e] <= mt_glob
       while (hi - lo > 1) {
@@ -310,6 +317,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     }
     e = __builtin_amdgcn_readfirstlane(e);
     row0 = __builtin_amdgcn_readfirstlane(row0);
+    mnat = __builtin_amdgcn_readfirstlane(mnat);
     valid = __builtin_amdgcn_readfirstlane(valid);
 
     // B (group 0 only): LDS row 32*i + ld_row holds weight row b_row0 + boff(i)
@@ -364,13 +372,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       const int k_steps_ = p.K / kBK;
       if (wave == 0) {
         mx_srd = make_srd(p.a_scale, static_cast<uint32_t>(k_steps_ * p.as_rs * 4));
-        mx_voff = (row0 + lane * 4) * 4;
+        mx_voff = (mnat * kBM + lane * 4) * 4;
         mx_kstride = static_cast<int>(p.as_rs) * 4;
         mx_lds = 2 * kTileBytes;
-      } else {
+      } else if (dense) {
         mx_srd = make_srd(p.b_scale, static_cast<uint32_t>(k_steps_ * p.nb * 4));
         mx_voff = (nt * kBN + lane * 4) * 4;
         mx_kstride = p.nb * 4;
+        mx_lds = 2 * kTileBytes + kScaleBytes;
+      } else {
+        // this B tile's words: k_steps_ consecutive KiB
+        const int ntiles = p.nb / kBN;
+        mx_srd = make_srd(reinterpret_cast<const uint8_t*>(p.b_scale) +
+                              (static_cast<int64_t>(e) * ntiles + nt) * k_steps_ * 1024,
+                          static_cast<uint32_t>(k_steps_) * 1024);
+        mx_voff = lane * 16;
+        mx_kstride = 1024;
         mx_lds = 2 * kTileBytes + kScaleBytes;
       }
     }
@@ -656,6 +673,52 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
           m = wave_max(m);
           if (lane == 0 && p.amax != nullptr)
             atomicMax(reinterpret_cast<unsigned int*>(p.amax), __float_as_uint(m));
+        } else if constexpr (EPI == Epi::kSiluMx) {
+          // MX requantisation of the bf16 h: per row and 32-column block,
+          // e = exponent field of amax (clamped to 254), q = e4m3(h * 2^(127-e))
+          // (the quant_mx_kernel rule).  The tile's 128 columns are one K step
+          // (nt) of the next GEMM; the block exponents of its rows are gathered
+          // in LDS and written as that GEMM's packed words of M tile mnat
+          // (word q, byte g: row 64*(q/64) + 16g + q%16, block (q%64)/16).
+          uint8_t* ex = smem + kBM * kCtLdSilu * 2;  // [256 rows][4 blocks]
+          uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * 128 + half * 64;
+#pragma unroll
+          for (int b = 0; b < 2; ++b) {
+            uint32_t ebits = 0;
+            if (r < valid) {
+              uint4 v[4];
+              float am = 0.0f;
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                v[u] = *reinterpret_cast<const uint4*>(src + b * 32 + u * 8);
+                const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                  am = fmaxf(am, fmaxf(fabsf(bf16_bits_to_f32(w[q] & 0xffffu)), fabsf(bf16_bits_to_f32(w[q] >> 16))));
+              }
+              ebits = min((__float_as_uint(am) >> 23) & 0xffu, 254u);
+              const int sh = 127 - static_cast<int>(ebits);
+              auto qv = [&](uint32_t h) { return __builtin_amdgcn_ldexpf(bf16_bits_to_f32(h), sh); };
+              uint32_t qw[8];
+#pragma unroll
+              for (int u = 0; u < 4; ++u) {
+                qw[2 * u] = pack_e4m3x4(qv(v[u].x & 0xffffu), qv(v[u].x >> 16), qv(v[u].y & 0xffffu), qv(v[u].y >> 16));
+                qw[2 * u + 1] = pack_e4m3x4(qv(v[u].z & 0xffffu), qv(v[u].z >> 16), qv(v[u].w & 0xffffu), qv(v[u].w >> 16));
+              }
+              *reinterpret_cast<uint4*>(dst + b * 32) = uint4{qw[0], qw[1], qw[2], qw[3]};
+              *reinterpret_cast<uint4*>(dst + b * 32 + 16) = uint4{qw[4], qw[5], qw[6], qw[7]};
+            }
+            ex[r * 4 + half * 2 + b] = static_cast<uint8_t>(ebits);  // 0 for rows past valid
+          }
+          __syncthreads();
+          if (tid < kBM) {
+            const int q = tid;
+            const int rr = (q & ~63) + (q & 15), ks = (q >> 4) & 3;
+            uint32_t w = 0;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) w |= static_cast<uint32_t>(ex[(rr + 16 * g) * 4 + ks]) << (8 * g);
+            reinterpret_cast<uint32_t*>(p.c_scale)[static_cast<int64_t>(nt) * p.cs_rs + static_cast<int64_t>(mnat) * kBM + q] = w;
+          }
         } else {
           // 1x128 group = the row's 128 columns of this tile
           m = fmaxf(m, __shfl_xor(m, 1, 64));

@@ -495,4 +495,76 @@ __global__ __launch_bounds__(256) void mx_pack_scales_kernel(const uint8_t* __re
   }
 }
 
+// Weight exponents e8m0 [E, nb, K/32] -> the grouped MX GEMM's words, per B
+// tile: [E][nb/256][K/128][256], word p of (expert e, N tile nt, K step kt)
+// holds in byte g the exponent of B-tile row R = 64*(p/64) + 16g + p%16 for K
+// block 4kt + (p%64)/16.  B-tile row R is weight row nt*256 + R, or for the
+// fused gate/up weights (gate_up = I) row nt*128 + 32*(R>>6) + (R&31) +
+// ((R>>5)&1)*I: the row order of pack_weights_kernel's stage images.
+__global__ __launch_bounds__(256) void mx_pack_weight_words_kernel(const uint8_t* __restrict__ s, int64_t nb,
+                                                                   int K, int gate_up,
+                                                                   uint32_t* __restrict__ out,
+                                                                   int64_t words) {
+  const int ks = K / 128, kb = K / 32;
+  const int64_t ntile = nb / 256;
+  for (int64_t w = blockIdx.x * 256ll + threadIdx.x; w < words; w += static_cast<int64_t>(gridDim.x) * 256) {
+    const int pos = static_cast<int>(w & 255);
+    const int64_t t = w >> 8;
+    const int kt = static_cast<int>(t % ks);
+    const int64_t tile = t / ks;
+    const int64_t e = tile / ntile;
+    const int nt = static_cast<int>(tile - e * ntile);
+    const int blk = 4 * kt + ((pos >> 4) & 3);
+    uint32_t v = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int R = (pos & ~63) + 16 * g + (pos & 15);
+      const int64_t wrow = gate_up ? nt * 128 + 32 * (R >> 6) + (R & 31) + ((R >> 5) & 1) * gate_up
+                                   : static_cast<int64_t>(nt) * 256 + R;
+      v |= static_cast<uint32_t>(s[(e * nb + wrow) * kb + blk]) << (8 * g);
+    }
+    out[w] = v;
+  }
+}
+
+// Activation exponents e8m0 [x_rows, K/32] -> tile-aligned words in expert
+// order: [K/128][ws_rs], word m*256 + q of K step kt (M tile m in expert order,
+// first row row0, `valid` rows) holds in byte g the exponent of tile row
+// r = 64*(q/64) + 16g + q%16 -- output row row0 + r, read from x row
+// gather[row0 + r] / gather_div (or row0 + r) -- for K block 4kt + (q%64)/16;
+// 0 for r >= valid.
+__global__ __launch_bounds__(256) void mx_gather_words_kernel(const uint8_t* __restrict__ s, int K,
+                                                              const int32_t* __restrict__ gather, int gather_div,
+                                                              const int32_t* __restrict__ offsets,
+                                                              const int32_t* __restrict__ mtile_offsets,
+                                                              int num_experts, int64_t ws_rs,
+                                                              uint32_t* __restrict__ out) {
+  const int kb = K / 32, ks = K / 128;
+  const int64_t n_words = static_cast<int64_t>(mtile_offsets[num_experts]) * 256;
+  const int64_t total = n_words * ks;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int kt = static_cast<int>(i / n_words);
+    const int64_t w = i - static_cast<int64_t>(kt) * n_words;
+    const int m = static_cast<int>(w >> 8), q = static_cast<int>(w & 255);
+    int lo = 0, hi = num_experts;  // largest e with mtile_offsets[e] <= m
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (mtile_offsets[mid] <= m) lo = mid; else hi = mid;
+    }
+    const int row0 = offsets[lo] + (m - mtile_offsets[lo]) * 256;
+    const int valid = min(256, offsets[lo + 1] - row0);
+    const int blk = 4 * kt + ((q >> 4) & 3);
+    uint32_t v = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int r = (q & ~63) + 16 * g + (q & 15);
+      if (r < valid) {
+        const int64_t xr = gather ? gather[row0 + r] / gather_div : row0 + r;
+        v |= static_cast<uint32_t>(s[xr * kb + blk]) << (8 * g);
+      }
+    }
+    out[static_cast<int64_t>(kt) * ws_rs + w] = v;
+  }
+}
+
 }  // namespace hkmoe

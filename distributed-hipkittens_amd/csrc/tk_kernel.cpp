@@ -464,6 +464,145 @@ void dispatch_gemm_mx(py::object A, py::object sa, py::object B, py::object sb, 
   check(hkmoe_gemm_mx(a.ptr, as.ptr, b.ptr, bs.ptr, c.ptr, m, n, k, out, current_stream()));
 }
 
+// MX MoE layer: e8m0 bytes are uint8 tensors, packed exponent words int32.
+int64_t mx_ws(int64_t rows, int64_t e) { return hkmoe_mx_words_per_step(rows, static_cast<int32_t>(e)); }
+
+void dispatch_mx_pack_weight_scales(py::object s, py::object words, int32_t gate_up) {
+  auto ss = as_tensor(s, "s"), ww = as_tensor(words, "words");
+  want_dtype(ss, "s", kU8);
+  want_dtype(ww, "words", kI32);
+  want_dim(ss, "s", 3);
+  const int64_t e = ss.shape[0], n = ss.shape[1], k = ss.shape[2] * 32;
+  if (ww.numel() != e * n * (k / 128)) throw std::runtime_error("words must hold E*N*K/128 ints");
+  check(hkmoe_mx_pack_weight_scales(ss.ptr, e, n, k, gate_up, ww.ptr, current_stream()));
+}
+
+void dispatch_mx_gather_scales(py::object s, py::object gather, int32_t gather_div, py::object offsets,
+                               py::object mtile_offsets, int64_t rows, py::object words) {
+  auto ss = as_tensor(s, "s"), g = as_tensor_opt(gather, "gather"), o = as_tensor(offsets, "offsets"),
+       mo = as_tensor(mtile_offsets, "mtile_offsets"), ww = as_tensor(words, "words");
+  want_dtype(ss, "s", kU8);
+  want_dtype(g, "gather", kI32);
+  want_dtype(ww, "words", kI32);
+  want_dim(ss, "s", 2);
+  const int64_t x_rows = ss.shape[0], k = ss.shape[1] * 32, e = o.numel() - 1;
+  if (mo.numel() != e + 1) throw std::runtime_error("offsets and mtile_offsets must hold E+1 values");
+  if (g.ptr && g.numel() != rows) throw std::runtime_error("gather must hold one index per row");
+  if (ww.numel() != (k / 128) * mx_ws(rows, e)) throw std::runtime_error("words must be [K/128, ws]");
+  check(hkmoe_mx_gather_scales(ss.ptr, x_rows, static_cast<int32_t>(k), static_cast<const int32_t*>(g.ptr),
+                               gather_div, static_cast<const int32_t*>(o.ptr),
+                               static_cast<const int32_t*>(mo.ptr), static_cast<int32_t>(e), rows, ww.ptr,
+                               current_stream()));
+}
+
+void dispatch_grouped_gemm1_mx(py::object x_q, py::object x_words, py::object gather, int32_t gather_div,
+                               py::object w13, py::object w13_words, py::object offsets,
+                               py::object mtile_offsets, py::object h, py::object h_words,
+                               py::object tile_counters, bool packed, py::object mtile_list) {
+  auto x = as_tensor(x_q, "x"), xw = as_tensor(x_words, "x_words"), gth = as_tensor_opt(gather, "gather"),
+       w = as_tensor(w13, "w13"), ww = as_tensor(w13_words, "w13_words"), o = as_tensor(offsets, "offsets"),
+       mo = as_tensor(mtile_offsets, "mtile_offsets"), hh = as_tensor(h, "h"),
+       hw = as_tensor_opt(h_words, "h_words"), tc = as_tensor_opt(tile_counters, "tile_counters"),
+       ml = as_tensor_opt(mtile_list, "mtile_list");
+  want_dtype(x, "x", kF8);
+  want_dtype(w, "w13", kF8);
+  want_dtype(xw, "x_words", kI32);
+  want_dtype(ww, "w13_words", kI32);
+  want_dtype(hw, "h_words", kI32);
+  want_dtype(gth, "gather", kI32);
+  want_dtype(tc, "tile_counters", kI32);
+  want_dtype(ml, "mtile_list", kI32);
+  want_dim(x, "x", 2);
+  want_dim(w, "w13", 3);
+  want_dim(hh, "h", 2);
+  if (tc.ptr && tc.numel() < 8) throw std::runtime_error("tile_counters must hold 8 ints");
+  const int64_t x_rows = x.shape[0], hidden = x.shape[1], e = w.shape[0], inter = w.shape[1] / 2;
+  const int64_t rows = hh.shape[0];
+  if (w.shape[2] != hidden || w.shape[1] % 2) throw std::runtime_error("w13 must be [E, 2I, H]");
+  if (hh.shape[1] != inter) throw std::runtime_error("h must be [rows, I]");
+  if (gth.ptr && gth.numel() != rows) throw std::runtime_error("gather must hold one index per row");
+  if (ml.ptr && ml.numel() < mtile_list_ints(rows, e)) throw std::runtime_error("mtile_list too small");
+  if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
+  if (xw.numel() != (hidden / 128) * mx_ws(rows, e)) throw std::runtime_error("x_words must be [H/128, ws]");
+  if (ww.numel() != e * 2 * inter * (hidden / 128)) throw std::runtime_error("w13_words must hold E*2I*H/128 ints");
+  int fmt;
+  if (hh.dtype == kBf16) fmt = HKMOE_BF16;
+  else if (hh.dtype == kF8) fmt = HKMOE_E4M3;
+  else throw std::runtime_error("h: expected bfloat16 or float8_e4m3fn");
+  if (fmt == HKMOE_E4M3 && (!hw.ptr || hw.numel() != (inter / 128) * mx_ws(rows, e)))
+    throw std::runtime_error("e4m3 output needs h_words [I/128, ws]");
+  check(hkmoe_grouped_gemm1_mx(x.ptr, xw.ptr, static_cast<const int32_t*>(gth.ptr), gather_div, x_rows, w.ptr,
+                               ww.ptr, static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr),
+                               static_cast<const int32_t*>(ml.ptr), rows, static_cast<int32_t>(e),
+                               static_cast<int32_t>(hidden), static_cast<int32_t>(inter),
+                               packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, fmt, hh.ptr, hw.ptr,
+                               static_cast<int32_t*>(tc.ptr), current_stream()));
+}
+
+void dispatch_grouped_gemm2_mx(py::object hq, py::object hq_words, py::object w2, py::object w2_words,
+                               py::object offsets, py::object mtile_offsets, py::object y,
+                               py::object tile_counters, bool packed, py::object mtile_list) {
+  auto q = as_tensor(hq, "hq"), qw = as_tensor(hq_words, "hq_words"), w = as_tensor(w2, "w2"),
+       ww = as_tensor(w2_words, "w2_words"), o = as_tensor(offsets, "offsets"),
+       mo = as_tensor(mtile_offsets, "mtile_offsets"), yy = as_tensor(y, "y"),
+       tc = as_tensor_opt(tile_counters, "tile_counters"), ml = as_tensor_opt(mtile_list, "mtile_list");
+  want_dtype(q, "hq", kF8);
+  want_dtype(w, "w2", kF8);
+  want_dtype(qw, "hq_words", kI32);
+  want_dtype(ww, "w2_words", kI32);
+  want_dtype(yy, "y", kBf16);
+  want_dtype(tc, "tile_counters", kI32);
+  want_dtype(ml, "mtile_list", kI32);
+  want_dim(q, "hq", 2);
+  want_dim(w, "w2", 3);
+  if (tc.ptr && tc.numel() < 8) throw std::runtime_error("tile_counters must hold 8 ints");
+  const int64_t rows = q.shape[0], inter = q.shape[1], e = w.shape[0], hidden = w.shape[1];
+  if (w.shape[2] != inter) throw std::runtime_error("w2 must be [E, H, I]");
+  if (yy.numel() != rows * hidden) throw std::runtime_error("y must be [rows, H]");
+  if (o.numel() != e + 1 || mo.numel() != e + 1) throw std::runtime_error("offsets must hold E+1 values");
+  if (ml.ptr && ml.numel() < mtile_list_ints(rows, e)) throw std::runtime_error("mtile_list too small");
+  if (qw.numel() != (inter / 128) * mx_ws(rows, e)) throw std::runtime_error("hq_words must be [I/128, ws]");
+  if (ww.numel() != e * hidden * (inter / 128)) throw std::runtime_error("w2_words must hold E*H*I/128 ints");
+  check(hkmoe_grouped_gemm2_mx(q.ptr, qw.ptr, w.ptr, ww.ptr, static_cast<const int32_t*>(o.ptr),
+                               static_cast<const int32_t*>(mo.ptr), static_cast<const int32_t*>(ml.ptr), rows,
+                               static_cast<int32_t>(e), static_cast<int32_t>(hidden),
+                               static_cast<int32_t>(inter), packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, yy.ptr,
+                               static_cast<int32_t*>(tc.ptr), current_stream()));
+}
+
+void dispatch_moe_mx(py::object x_q, py::object x_e8m0, py::object logits, py::object w13, py::object w13_words,
+                     py::object w2, py::object w2_words, int32_t top_k, py::object out, py::object workspace,
+                     bool packed) {
+  auto x = as_tensor(x_q, "x_q"), xe = as_tensor(x_e8m0, "x_e8m0"), l = as_tensor(logits, "logits"),
+       a = as_tensor(w13, "w13"), aw = as_tensor(w13_words, "w13_words"), b = as_tensor(w2, "w2"),
+       bw = as_tensor(w2_words, "w2_words"), o = as_tensor(out, "out"), ws = as_tensor(workspace, "workspace");
+  want_dtype(x, "x_q", kF8);
+  want_dtype(a, "w13", kF8);
+  want_dtype(b, "w2", kF8);
+  want_dtype(xe, "x_e8m0", kU8);
+  want_dtype(aw, "w13_words", kI32);
+  want_dtype(bw, "w2_words", kI32);
+  want_dtype(l, "logits", kF32);
+  want_dtype(o, "out", kBf16);
+  want_dim(x, "x_q", 2);
+  want_dim(l, "logits", 2);
+  want_dim(a, "w13", 3);
+  want_dim(b, "w2", 3);
+  const int64_t t = x.shape[0], hidden = x.shape[1], e = a.shape[0], inter = a.shape[1] / 2;
+  if (l.shape[0] != t || l.shape[1] != e) throw std::runtime_error("logits must be [T, E]");
+  if (a.shape[2] != hidden || b.shape[0] != e || b.shape[1] != hidden || b.shape[2] != inter)
+    throw std::runtime_error("w13 must be [E, 2I, H] and w2 [E, H, I]");
+  if (o.numel() != t * hidden) throw std::runtime_error("out must be [T, H]");
+  if (xe.numel() != t * (hidden / 32)) throw std::runtime_error("x_e8m0 must be [T, H/32]");
+  if (aw.numel() != e * 2 * inter * (hidden / 128) || bw.numel() != e * hidden * (inter / 128))
+    throw std::runtime_error("weight words: w13_words E*2I*H/128, w2_words E*H*I/128 ints");
+  const size_t bytes = static_cast<size_t>(ws.numel()) * (ws.dtype == kF32 || ws.dtype == kI32 ? 4 : 1);
+  check(hkmoe_moe_forward_mx(x.ptr, xe.ptr, static_cast<const float*>(l.ptr), a.ptr, aw.ptr, b.ptr, bw.ptr, t,
+                             static_cast<int32_t>(e), top_k, static_cast<int32_t>(hidden),
+                             static_cast<int32_t>(inter), packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, o.ptr, ws.ptr,
+                             bytes, current_stream()));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(tk_kernel, m) {
@@ -496,6 +635,21 @@ PYBIND11_MODULE(tk_kernel, m) {
   m.def("dispatch_quant_tensor", &dispatch_quant_tensor);
   m.def("dispatch_quant_mx", &dispatch_quant_mx, "x fp32 [R,C] -> q e4m3 [R,C], e8m0 s uint8 [R,C/32]");
   m.def("dispatch_mx_pack_scales", &dispatch_mx_pack_scales, py::arg("s"), py::arg("cols"), py::arg("packed"));
+  m.def("mx_words_per_step", &mx_ws, "words per K step of the tile-aligned MX exponent layouts");
+  m.def("dispatch_mx_pack_weight_scales", &dispatch_mx_pack_weight_scales, py::arg("s"), py::arg("words"),
+        py::arg("gate_up"));
+  m.def("dispatch_mx_gather_scales", &dispatch_mx_gather_scales, py::arg("s"), py::arg("gather"),
+        py::arg("gather_div"), py::arg("offsets"), py::arg("mtile_offsets"), py::arg("rows"), py::arg("words"));
+  m.def("dispatch_grouped_gemm1_mx", &dispatch_grouped_gemm1_mx, py::arg("x_q"), py::arg("x_words"),
+        py::arg("gather"), py::arg("gather_div"), py::arg("w13"), py::arg("w13_words"), py::arg("offsets"),
+        py::arg("mtile_offsets"), py::arg("h"), py::arg("h_words") = py::none(),
+        py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none());
+  m.def("dispatch_grouped_gemm2_mx", &dispatch_grouped_gemm2_mx, py::arg("hq"), py::arg("hq_words"),
+        py::arg("w2"), py::arg("w2_words"), py::arg("offsets"), py::arg("mtile_offsets"), py::arg("y"),
+        py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none());
+  m.def("dispatch_moe_mx", &dispatch_moe_mx, py::arg("x_q"), py::arg("x_e8m0"), py::arg("logits"),
+        py::arg("w13"), py::arg("w13_words"), py::arg("w2"), py::arg("w2_words"), py::arg("top_k"),
+        py::arg("out"), py::arg("workspace"), py::arg("packed") = true);
   m.def("dispatch_gemm_mx", &dispatch_gemm_mx, "C = A . B^T with 1x32 e8m0 scales (packed words)",
         py::arg("A"), py::arg("scale_a"), py::arg("B"), py::arg("scale_b"), py::arg("C"));
   m.def("moe_workspace_size", &moe_workspace_size);
@@ -504,4 +658,5 @@ PYBIND11_MODULE(tk_kernel, m) {
   m.def("version", []() { return hkmoe_version(); });
   m.attr("SCALE_TENSOR") = static_cast<int>(HKMOE_SCALE_TENSOR);
   m.attr("SCALE_BLOCK") = static_cast<int>(HKMOE_SCALE_BLOCK);
+  m.attr("SCALE_MX") = static_cast<int>(HKMOE_SCALE_MX);
 }

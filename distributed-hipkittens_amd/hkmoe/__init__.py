@@ -30,12 +30,14 @@ except ImportError as exc:  # pragma: no cover - exercised only on a broken tree
     ) from exc
 
 from .layer import (MoELayer, moe_forward, moe_forward_steps, pack_weights,  # noqa: E402
-                    quant_block, quant_group, quant_tensor, gemm_fp8, quant_mx, mx_pack_scales, gemm_mx)
+                    quant_block, quant_group, quant_tensor, gemm_fp8, quant_mx, mx_pack_scales, gemm_mx,
+                    mx_pack_weight_scales, moe_forward_mx_steps, MoELayerMX)
 
 LIB_PATH = os.path.join(_PKG_ROOT, "libhkmoe.so")
 SCALE_TENSOR = tk_kernel.SCALE_TENSOR
 SCALE_BLOCK = tk_kernel.SCALE_BLOCK
 
 __all__ = ["tk_kernel", "MoELayer", "moe_forward", "moe_forward_steps", "pack_weights", "quant_block",
-           "quant_group", "quant_tensor", "gemm_fp8", "quant_mx", "mx_pack_scales", "gemm_mx", "LIB_PATH",
+           "quant_group", "quant_tensor", "gemm_fp8", "quant_mx", "mx_pack_scales", "gemm_mx",
+           "mx_pack_weight_scales", "moe_forward_mx_steps", "MoELayerMX", "LIB_PATH",
            "SCALE_TENSOR", "SCALE_BLOCK"]

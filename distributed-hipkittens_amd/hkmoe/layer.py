@@ -216,3 +216,107 @@ class MoELayer:
         ws = self.workspace(x_q.shape[0], x_q.device)
         return moe_forward(x_q, x_scale, logits, self.w13_q, self.w13_scale, self.w2_q,
                            self.w2_scale, self.top_k, out=out, workspace=ws, packed=self.packed)
+
+
+# ----------------------------------------------------------------------------
+# MX (1x32 e8m0) MoE layer
+# ----------------------------------------------------------------------------
+def mx_pack_weight_scales(s, gate_up=False):
+    """e8m0 weight exponents uint8 [E, N, K/32] -> the grouped MX GEMMs' words
+    (int32, [E, N/256, K/128, 256]); ``gate_up`` for the fused w13 [E, 2I, H/32]."""
+    _check_dev(s)
+    s = s.contiguous()
+    e, n, kb = s.shape
+    words = torch.empty((e, n // 256, kb // 4, 256), dtype=torch.int32, device=s.device)
+    tk_kernel.dispatch_mx_pack_weight_scales(s, words, n // 2 if gate_up else 0)
+    return words
+
+
+def moe_forward_mx_steps(x_q, x_e8m0, logits, w13_q, w13_words, w2_q, w2_words, top_k,
+                         keep_h=False, packed=False):
+    """The MX layer one kernel at a time; returns every intermediate (``xw``:
+    gathered activation words, ``hq``/``hw``: GEMM 1's e4m3 output and its
+    words; with ``keep_h`` also GEMM 1's bf16 h)."""
+    _check_dev(x_q, x_e8m0, logits, w13_q, w2_q)
+    dev = x_q.device
+    t, hidden = x_q.shape
+    e, two_i, _ = w13_q.shape
+    inter = two_i // 2
+    rows = t * top_k
+    ws = tk_kernel.mx_words_per_step(rows, e)
+    i32 = dict(dtype=torch.int32, device=dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    nblk = tk_kernel.route_blocks(t)
+    r = dict(
+        topk_idx=torch.empty((t, top_k), **i32), topk_w=torch.empty((t, top_k), **f32),
+        block_counts=torch.empty((nblk, e), **i32), block_base=torch.empty((nblk, e), **i32),
+        counts=torch.empty(e, **i32), offsets=torch.empty(e + 1, **i32),
+        mtile_offsets=torch.empty(e + 1, **i32), amax=torch.empty(1, **f32),
+        mtile_list=torch.empty(tk_kernel.mtile_list_ints(t * min(e, 32), e), **i32),
+        tile_ctr=torch.empty(16, **i32),
+        perm=torch.empty(rows, **i32), inv_perm=torch.empty(rows, **i32),
+        xw=torch.empty((hidden // GROUP, ws), **i32),
+        hq=torch.empty((rows, inter), dtype=F8, device=dev),
+        hw=torch.empty((inter // GROUP, ws), **i32),
+        y=torch.empty((rows, hidden), dtype=torch.bfloat16, device=dev),
+        out=torch.empty((t, hidden), dtype=torch.bfloat16, device=dev),
+    )
+    tk_kernel.dispatch_route_topk(logits, r["topk_idx"], r["topk_w"], r["block_counts"])
+    tk_kernel.dispatch_expert_offsets(r["block_counts"], t, r["counts"], r["offsets"],
+                                      r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"],
+                                      r["mtile_list"])
+    tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"],
+                               r["inv_perm"], None, None, None, None)
+    tk_kernel.dispatch_mx_gather_scales(x_e8m0, r["perm"], top_k, r["offsets"], r["mtile_offsets"],
+                                        rows, r["xw"])
+    tk_kernel.dispatch_grouped_gemm1_mx(x_q, r["xw"], r["perm"], top_k, w13_q, w13_words, r["offsets"],
+                                        r["mtile_offsets"], r["hq"], r["hw"], r["tile_ctr"][:8],
+                                        packed=packed, mtile_list=r["mtile_list"])
+    if keep_h:  # static tile order for the inspection pass
+        r["h"] = torch.empty((rows, inter), dtype=torch.bfloat16, device=dev)
+        tk_kernel.dispatch_grouped_gemm1_mx(x_q, r["xw"], r["perm"], top_k, w13_q, w13_words,
+                                            r["offsets"], r["mtile_offsets"], r["h"], None, packed=packed)
+    tk_kernel.dispatch_grouped_gemm2_mx(r["hq"], r["hw"], w2_q, w2_words, r["offsets"], r["mtile_offsets"],
+                                        r["y"], r["tile_ctr"][8:], packed=packed, mtile_list=r["mtile_list"])
+    tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])
+    return r
+
+
+class MoELayerMX:
+    """MX FP8 MoE FFN layer: e4m3 expert weights with 1x32 e8m0 exponents
+    (uint8 [E, 2I, H/32] and [E, H, I/32]); activations come with their e8m0
+    exponents [T, H/32] (see :func:`quant_mx`).  Weights and their exponents
+    are packed once, here; each call is one hkmoe_moe_forward_mx."""
+
+    def __init__(self, w13_q, w13_e8m0, w2_q, w2_e8m0, top_k, pack=True):
+        _check_dev(w13_q, w2_q, w13_e8m0, w2_e8m0)
+        if w13_q.dtype != F8 or w2_q.dtype != F8:
+            raise RuntimeError("MoELayerMX: weights must be float8_e4m3fn")
+        if w13_e8m0.dtype != torch.uint8 or w2_e8m0.dtype != torch.uint8:
+            raise RuntimeError("MoELayerMX: weight exponents must be uint8 e8m0")
+        self.packed = bool(pack)
+        if self.packed:
+            self.w13_q, self.w2_q = pack_weights(w13_q, gate_up=True), pack_weights(w2_q)
+        else:
+            self.w13_q, self.w2_q = w13_q.contiguous(), w2_q.contiguous()
+        self.w13_words = mx_pack_weight_scales(w13_e8m0, gate_up=True)
+        self.w2_words = mx_pack_weight_scales(w2_e8m0)
+        self.top_k = int(top_k)
+        self.num_experts, two_i, self.hidden = w13_q.shape
+        self.inter = two_i // 2
+        self._ws = None
+
+    def workspace(self, num_tokens, device):
+        need = tk_kernel.moe_workspace_size(num_tokens, self.num_experts, self.top_k, self.hidden,
+                                            self.inter, tk_kernel.SCALE_MX)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return self._ws
+
+    def __call__(self, x_q, x_e8m0, logits, out=None):
+        t = x_q.shape[0]
+        if out is None:
+            out = torch.empty((t, self.hidden), dtype=torch.bfloat16, device=x_q.device)
+        tk_kernel.dispatch_moe_mx(x_q, x_e8m0, logits, self.w13_q, self.w13_words, self.w2_q, self.w2_words,
+                                  self.top_k, out, self.workspace(t, x_q.device), packed=self.packed)
+        return out

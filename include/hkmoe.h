@@ -42,7 +42,8 @@ enum hkmoe_dtype { HKMOE_BF16 = 0, HKMOE_F32 = 1, HKMOE_E4M3 = 2 };
 
 enum hkmoe_scale_mode {
   HKMOE_SCALE_TENSOR = 0, /* one fp32 scale per tensor (weights: one per expert) */
-  HKMOE_SCALE_BLOCK = 1   /* activations 1x128 groups, weights 128x128 blocks */
+  HKMOE_SCALE_BLOCK = 1,  /* activations 1x128 groups, weights 128x128 blocks */
+  HKMOE_SCALE_MX = 2      /* 1x32 e8m0 exponents on both operands (MX layer entry points) */
 };
 
 /* Byte layout of expert weights [E, N, K] given to the grouped GEMMs. */
@@ -198,6 +199,8 @@ int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, i
  *   logits [T,E] fp32; w13/w2 and scales as above, both in w_layout; out [T,H]
  *   bf16.  workspace: device buffer of hkmoe_moe_workspace_size(...) bytes,
  *   256-byte aligned, holding every intermediate (routing, permutation, h, y).
+ *   hkmoe_moe_workspace_size also sizes hkmoe_moe_forward_mx's workspace with
+ *   scale_mode HKMOE_SCALE_MX (0 for an unknown mode).
  */
 size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k,
                                 int32_t hidden, int32_t inter, int scale_mode);
@@ -259,6 +262,62 @@ int hkmoe_mx_pack_scales(const void* s, int64_t rows, int64_t cols, void* packed
  */
 int hkmoe_gemm_mx(const void* a, const void* a_scale, const void* b, const void* b_scale, void* c,
                   int64_t m, int64_t n, int64_t k, int out_dtype, hkmoe_stream_t stream);
+
+/*
+ * MX (1x32 e8m0) mixture-of-experts layer: the same routing, grouped GEMMs and
+ * combine as hkmoe_moe_forward, with MX operands instead of fp32 scales.  The
+ * exponents are applied inside the scaled MFMA, so the grouped GEMMs carry no
+ * per-K-block rescale of their accumulators.  The reference applies MX scales
+ * in its dense MXFP8 kernel only (kernels/cdna4/gemm/mxfp8/MXFP8_4wave/
+ * 4_wave.cu:77-292); these entry points have no counterpart there.
+ *
+ * Exponent word layouts (uint32, byte g of a word = one e8m0 exponent):
+ *   tile-aligned activation words, [K/128][ws] with ws =
+ *     hkmoe_mx_words_per_step(rows, E): M tile m (expert order, first row row0)
+ *     owns words m*256 .. m*256+255; word m*256+q of K step kt holds in byte g
+ *     the exponent of row row0 + 64*(q/64) + 16g + q%16 for K block
+ *     4kt + (q%64)/16 (0 past the tile's rows).
+ *   weight words, per B tile: [E][N/256][K/128][256]; word p of (expert e, N
+ *     tile nt, K step kt) holds in byte g the exponent of B-tile row
+ *     R = 64*(p/64) + 16g + p%16 for K block 4kt + (p%64)/16, where B-tile row R
+ *     is weight row nt*256 + R, or with gate_up = I the fused gate/up row
+ *     nt*128 + 32*(R>>6) + (R&31) + ((R>>5)&1)*I.
+ *
+ * hkmoe_mx_words_per_step: ws for `rows` expert rows over E experts.
+ * hkmoe_mx_pack_weight_scales: e8m0 [E, N, K/32] -> weight words (load time).
+ * hkmoe_mx_gather_scales: e8m0 of x [x_rows, K/32] -> tile-aligned words of the
+ *   expert-ordered rows (row p read from x row gather[p] / gather_div, or p).
+ * hkmoe_grouped_gemm1_mx: as hkmoe_grouped_gemm1 (x read in place through
+ *   gather), out_format HKMOE_BF16: h bf16 [rows, I]; HKMOE_E4M3: h e4m3 [rows, I]
+ *   requantised per 1x32 block (the hkmoe_quant_mx rule applied to the bf16 h)
+ *   and its tile-aligned words h_words [I/128][ws].
+ * hkmoe_grouped_gemm2_mx: y bf16 [rows, H] from hq e4m3 + hq_words and w2.
+ * hkmoe_moe_forward_mx: the whole layer; x_e8m0 [T, H/32] bytes (from
+ *   hkmoe_quant_mx), weight words from hkmoe_mx_pack_weight_scales; workspace
+ *   from hkmoe_moe_workspace_size(..., HKMOE_SCALE_MX).
+ */
+int64_t hkmoe_mx_words_per_step(int64_t rows, int32_t num_experts);
+int hkmoe_mx_pack_weight_scales(const void* s, int64_t num_experts, int64_t n, int64_t k, int32_t gate_up,
+                                void* words, hkmoe_stream_t stream);
+int hkmoe_mx_gather_scales(const void* s, int64_t x_rows, int32_t k, const int32_t* gather,
+                           int32_t gather_div, const int32_t* offsets, const int32_t* mtile_offsets,
+                           int32_t num_experts, int64_t rows, void* words, hkmoe_stream_t stream);
+int hkmoe_grouped_gemm1_mx(const void* x, const void* x_words, const int32_t* gather, int32_t gather_div,
+                           int64_t x_rows, const void* w13, const void* w13_words, const int32_t* offsets,
+                           const int32_t* mtile_offsets, const int32_t* mtile_list, int64_t rows,
+                           int32_t num_experts, int32_t hidden, int32_t inter, int w_layout,
+                           int out_format, void* h, void* h_words, int32_t* tile_counters,
+                           hkmoe_stream_t stream);
+int hkmoe_grouped_gemm2_mx(const void* hq, const void* hq_words, const void* w2, const void* w2_words,
+                           const int32_t* offsets, const int32_t* mtile_offsets,
+                           const int32_t* mtile_list, int64_t rows, int32_t num_experts,
+                           int32_t hidden, int32_t inter, int w_layout, void* y,
+                           int32_t* tile_counters, hkmoe_stream_t stream);
+int hkmoe_moe_forward_mx(const void* x_q, const void* x_e8m0, const float* logits, const void* w13,
+                         const void* w13_words, const void* w2, const void* w2_words,
+                         int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
+                         int32_t inter, int w_layout, void* out, void* workspace,
+                         size_t workspace_bytes, hkmoe_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -130,3 +130,109 @@ def make_mx_dense(M, N, K, seed=42, sigma=0.5):
     a_q, sa = quant_mx(a)
     b_q, sb = quant_mx(b)
     return dict(a=a, b=b, a_q=a_q, sa=sa, b_q=b_q, sb=sb)
+
+
+# ----------------------------------------------------------------------------
+# MX mixture-of-experts layer (this path's specification; the reference has no
+# MoE code).  Routing, permutation, SiLU*up and combine are spec.py's.
+# ----------------------------------------------------------------------------
+TILE_M = 256
+
+
+def tile_words_per_step(rows, num_experts):
+    """Words per K step of the tile-aligned exponent layouts."""
+    return ((rows + TILE_M - 1) // TILE_M + num_experts) * TILE_M
+
+
+def gather_words(s_rows, offsets, num_experts):
+    """Tile-aligned activation words [K/128, ws] from the exponents of the
+    expert-ordered rows s_rows [rows, K/32]: M tile m of expert e (first row
+    offsets[e] + 256*j) owns words m*256 .. +255; word m*256 + q of step kt holds
+    in byte g the exponent of the tile's row 64*(q//64) + 16g + q%16 for block
+    4kt + (q%64)//16, 0 past the expert's rows.  Written as loops over tiles
+    and bytes, independently of the kernel's index arithmetic."""
+    rows, kb = s_rows.shape
+    ws = tile_words_per_step(rows, num_experts)
+    out = np.zeros((kb // 4, ws), dtype=np.uint32)
+    m = 0
+    for e in range(num_experts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        for row0 in range(lo, hi, TILE_M):
+            tile = np.zeros((TILE_M, kb), dtype=np.uint32)
+            n = min(TILE_M, hi - row0)
+            tile[:n] = s_rows[row0:row0 + n]
+            for q in range(TILE_M):
+                for g in range(4):
+                    r = (q // 64) * 64 + 16 * g + q % 16
+                    out[:, m * TILE_M + q] |= tile[r, ((q % 64) // 16)::4] << np.uint32(8 * g)
+            m += 1
+    return out
+
+
+def pack_weight_words(s, gate_up=0):
+    """Weight words [E, N/256, K/128, 256] from e8m0 s [E, N, K/32]: word p of
+    (e, nt, kt) holds in byte g the exponent of B-tile row R = 64*(p//64) +
+    16g + p%16 (weight row nt*256 + R, or with gate_up = I the gate/up row
+    nt*128 + 32*(R//64) + R%32 + ((R//32)%2)*I) for block 4kt + (p%64)//16."""
+    s = np.asarray(s, dtype=np.uint8)
+    e_n, n, kb = s.shape
+    out = np.zeros((e_n, n // 256, kb // 4, 256), dtype=np.uint32)
+    for nt in range(n // 256):
+        for p in range(256):
+            for g in range(4):
+                R = (p // 64) * 64 + 16 * g + p % 16
+                wrow = (nt * 128 + 32 * (R // 64) + R % 32 + ((R // 32) % 2) * gate_up) if gate_up \
+                    else nt * 256 + R
+                out[:, nt, :, p] |= s[:, wrow, ((p % 64) // 16)::4].astype(np.uint32) << np.uint32(8 * g)
+    return out
+
+
+def moe_forward_mx(x_q, x_e8m0, logits, w13_q, w13_e8m0, w2_q, w2_e8m0, k, return_all=False):
+    """MX layer: route -> permute -> GEMM1 (MX operands) + SiLU*up -> bf16 h ->
+    MX requantisation (quant_mx) -> GEMM2 (MX operands) -> bf16 y -> combine."""
+    from . import spec
+    e_n = w13_q.shape[0]
+    idx, w = spec.route_topk(logits, k)
+    counts, offsets = spec.expert_counts_offsets(idx, e_n)
+    perm, inv = spec.permutation(idx, e_n)
+    xp = x_q[perm // k]
+    xs = x_e8m0[perm // k]
+    rows = xp.shape[0]
+    inter = w13_q.shape[1] // 2
+    hidden = w2_q.shape[1]
+    z = np.zeros((rows, 2 * inter), dtype=np.float32)
+    for e in range(e_n):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi > lo:
+            z[lo:hi] = (dequant_mx(xp[lo:hi], xs[lo:hi]) @ dequant_mx(w13_q[e], w13_e8m0[e]).T).astype(np.float32)
+    h = bf16_round(spec.silu_mul(z[:, :inter], z[:, inter:]))
+    hq, hs = quant_mx(h)
+    y = np.zeros((rows, hidden), dtype=np.float32)
+    for e in range(e_n):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi > lo:
+            y[lo:hi] = (dequant_mx(hq[lo:hi], hs[lo:hi]) @ dequant_mx(w2_q[e], w2_e8m0[e]).T).astype(np.float32)
+    y = bf16_round(y)
+    out_f32 = spec.combine(y, w, inv, rounded=False)
+    out = bf16_round(out_f32)
+    if return_all:
+        return dict(topk_idx=idx, topk_w=w, counts=counts, offsets=offsets, perm=perm, inv_perm=inv,
+                    xs=xs, h=h, hq=hq, hs=hs, y=y, out=out, out_f32=out_f32)
+    return out
+
+
+def make_mx_moe(T, H, I, E, k, skew, seed=0):
+    """Seeded MX layer inputs: N(0,1) activations and weights quantised by
+    quant_mx (weights per expert row), logits as oracle.synth.make_logits."""
+    from .synth import make_logits
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = make_logits(rng, T, E, skew)
+    w13 = rng.standard_normal((E, 2 * I, H)).astype(np.float32)
+    w2 = rng.standard_normal((E, H, I)).astype(np.float32)
+    x_q, x_e = quant_mx(x)
+    w13_q, w13_e = quant_mx(w13.reshape(E * 2 * I, H))
+    w2_q, w2_e = quant_mx(w2.reshape(E * H, I))
+    return dict(x_q=x_q, x_e8m0=x_e, logits=logits, k=k,
+                w13_q=w13_q.reshape(E, 2 * I, H), w13_e8m0=w13_e.reshape(E, 2 * I, H // 32),
+                w2_q=w2_q.reshape(E, H, I), w2_e8m0=w2_e.reshape(E, H, I // 32))

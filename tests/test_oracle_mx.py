@@ -187,3 +187,72 @@ def test_planted_mx_mistakes_are_caught(monkeypatch):
         mx.dequant_mx(a_q, sa) @ mx.dequant_mx(b_q, np.resize(sa, sb.shape)).T).astype(np.float32))
     with pytest.raises(AssertionError):
         check_gemm(mx)
+
+
+# ----------------------------------------------------------------------------
+# MX MoE layer oracle
+# ----------------------------------------------------------------------------
+def _pad_rows(a, n):
+    out = np.zeros((n, a.shape[1]), dtype=a.dtype)
+    out[:a.shape[0]] = a
+    return out
+
+
+def test_gather_words_tile_by_tile_vs_pack():
+    """Each M tile's 256 words equal mx_pack_scales of that tile's rows (padded
+    to 256 with zeros), which is pinned against the reference's packing."""
+    rng = np.random.default_rng(7)
+    counts = np.array([0, 300, 17, 256, 513, 1], dtype=np.int64)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    rows = int(offsets[-1])
+    s = rng.integers(1, 255, (rows, 8), dtype=np.uint8)
+    words = mx.gather_words(s, offsets, len(counts))
+    m = 0
+    for e in range(len(counts)):
+        for row0 in range(int(offsets[e]), int(offsets[e + 1]), 256):
+            n = min(256, int(offsets[e + 1]) - row0)
+            np.testing.assert_array_equal(words[:, m * 256:(m + 1) * 256],
+                                          mx.mx_pack_scales(_pad_rows(s[row0:row0 + n], 256)))
+            m += 1
+    assert not words[:, m * 256:].any()
+
+
+def test_pack_weight_words_vs_pack():
+    rng = np.random.default_rng(8)
+    s = rng.integers(1, 255, (3, 512, 16), dtype=np.uint8)
+    w = mx.pack_weight_words(s)
+    for e in range(3):
+        for nt in range(2):
+            np.testing.assert_array_equal(w[e, nt], mx.mx_pack_scales(s[e, nt * 256:(nt + 1) * 256]))
+    # fused gate/up rows: 64-row quarter q of B tile nt holds gate rows
+    # nt*128 + 32q .. +31, then the matching up rows (+I)
+    I = 256
+    wg = mx.pack_weight_words(s, gate_up=I)
+    for e in range(3):
+        for nt in range(2):
+            rows = [nt * 128 + 32 * (R // 64) + (R % 32) + (I if (R // 32) % 2 else 0) for R in range(256)]
+            np.testing.assert_array_equal(wg[e, nt], mx.mx_pack_scales(s[e, rows]))
+
+
+def test_moe_forward_mx_vs_per_token_bruteforce():
+    """Per token, without permutation or grouped GEMMs: out[t] = bf16(sum_j
+    w_j * bf16(deq(quant_mx(bf16(silu(g)*u))) . deq(W2[e_j])^T))."""
+    from oracle import brute
+    d = mx.make_mx_moe(T=20, H=256, I=128, E=6, k=3, skew=True, seed=9)
+    r = mx.moe_forward_mx(d["x_q"], d["x_e8m0"], d["logits"], d["w13_q"], d["w13_e8m0"], d["w2_q"],
+                          d["w2_e8m0"], 3, return_all=True)
+    I = 128
+    out = np.zeros((20, 256), dtype=np.float32)
+    for t in range(20):
+        sel, wts = brute.topk_bruteforce(d["logits"][t], 3)
+        xt = mx.dequant_mx(d["x_q"][t:t + 1], d["x_e8m0"][t:t + 1])
+        acc = np.float32(0) * np.zeros(256, np.float32)
+        for j, e in enumerate(sel):
+            z = (xt @ mx.dequant_mx(d["w13_q"][e], d["w13_e8m0"][e]).T).astype(np.float32)
+            h = fp8.bf16_round(spec.silu_mul(z[:, :I], z[:, I:]))
+            hq, hs = mx.quant_mx(h)
+            y = fp8.bf16_round((mx.dequant_mx(hq, hs) @ mx.dequant_mx(d["w2_q"][e], d["w2_e8m0"][e]).T)
+                               .astype(np.float32))
+            acc = (acc + np.float32(wts[j]) * y[0]).astype(np.float32)
+        out[t] = fp8.bf16_round(acc)
+    np.testing.assert_array_equal(r["out"], out)
