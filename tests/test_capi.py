@@ -140,6 +140,30 @@ def test_mx_argument_errors(lib):
     assert lib.hkmoe_gemm_mx(fake, fake, fake, fake, fake, i64(0), i64(256), i64(128), 1, None) == 0
 
 
+def test_mx_moe_argument_errors(lib):
+    fake, other = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000)
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    lib.hkmoe_mx_words_per_step.restype = ctypes.c_int64
+    assert lib.hkmoe_mx_words_per_step(i64(65536), i32(256)) == (256 + 256) * 256
+    assert lib.hkmoe_mx_words_per_step(i64(1), i32(4)) == (1 + 4) * 256
+    assert lib.hkmoe_moe_workspace_size(i64(64), 8, 2, 256, 128, 7) == 0  # unknown scale mode
+    assert lib.hkmoe_moe_workspace_size(i64(64), 8, 2, 256, 128, 2) > 0   # HKMOE_SCALE_MX
+    assert lib.hkmoe_mx_pack_weight_scales(fake, i64(2), i64(384), i64(256), i32(0), other, None) == 1
+    assert "multiple of 256" in _err(lib)
+    assert lib.hkmoe_mx_pack_weight_scales(fake, i64(2), i64(512), i64(256), i32(128), other, None) == 1
+    assert "gate_up" in _err(lib)
+    rc = lib.hkmoe_grouped_gemm1_mx(fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, None, i64(128),
+                                    i32(8), i32(256), i32(128), 1, 9, fake, fake, None, None)
+    assert rc == 1 and "out_format" in _err(lib)
+    rc = lib.hkmoe_grouped_gemm2_mx(fake, fake, fake, fake, fake, fake, None, i64(128), i32(8), i32(200),
+                                    i32(128), 1, fake, None, None)
+    assert rc == 1 and "multiple of 256" in _err(lib)
+    ws = lib.hkmoe_moe_workspace_size(i64(64), 8, 2, 256, 128, 2)
+    args = [fake, fake, fake, fake, fake, fake, fake, i64(64), i32(8), i32(2), i32(256), i32(128), 1, fake,
+            fake, ctypes.c_size_t(ws - 1), None]
+    assert lib.hkmoe_moe_forward_mx(*args) == 4  # HKMOE_ERR_WORKSPACE
+
+
 def _align(x):
     return (x + 255) // 256 * 256
 
