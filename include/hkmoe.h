@@ -276,7 +276,8 @@ int hkmoe_gemm_mx(const void* a, const void* a_scale, const void* b, const void*
  *     hkmoe_mx_words_per_step(rows, E): M tile m (expert order, first row row0)
  *     owns words m*256 .. m*256+255; word m*256+q of K step kt holds in byte g
  *     the exponent of row row0 + 64*(q/64) + 16g + q%16 for K block
- *     4kt + (q%64)/16 (0 past the tile's rows).
+ *     4kt + (q%64)/16 (0 past the tile's rows).  Words past the last M tile
+ *     are neither written nor read.
  *   weight words, per B tile: [E][N/256][K/128][256]; word p of (expert e, N
  *     tile nt, K step kt) holds in byte g the exponent of B-tile row
  *     R = 64*(p/64) + 16g + p%16 for K block 4kt + (p%64)/16, where B-tile row R

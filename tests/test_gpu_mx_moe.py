@@ -71,8 +71,11 @@ def test_mx_layer_stepwise(hk, name):
     np.testing.assert_array_equal(r["perm"].cpu().numpy(), ref["perm"])
     rows, e = int(ref["offsets"][-1]), CASES[name]["E"]
     ws = mx.tile_words_per_step(rows, e)
-    # gathered activation words
-    np.testing.assert_array_equal(_words(r["xw"]), mx.gather_words(ref["xs"], ref["offsets"], e))
+    # gathered activation words (written for the M tiles that exist; the rest of
+    # the ws words per step are never read)
+    n_mt = int(r["mtile_offsets"].cpu().numpy()[-1])
+    used = slice(0, n_mt * 256)
+    np.testing.assert_array_equal(_words(r["xw"])[:, used], mx.gather_words(ref["xs"], ref["offsets"], e)[:, used])
     # GEMM 1's h against the oracle's fp32 value, and the fused requantisation
     # against quant_mx of the GPU's own bf16 h (bit-exact, words included)
     h_gpu = bf16_np(r["h"])
@@ -81,7 +84,7 @@ def test_mx_layer_stepwise(hk, name):
     np.testing.assert_array_equal(f8_np(r["hq"]), hq_ref)
     hw = _words(r["hw"])
     assert hw.shape == (CASES[name]["I"] // 128, ws)
-    np.testing.assert_array_equal(hw, mx.gather_words(hs_ref, ref["offsets"], e))
+    np.testing.assert_array_equal(hw[:, used], mx.gather_words(hs_ref, ref["offsets"], e)[:, used])
     # GEMM 2 from the GPU's own hq: within tolerance of the fp32 product
     offs = ref["offsets"]
     y_ref = np.zeros((rows, CASES[name]["H"]), np.float32)
