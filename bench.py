@@ -67,6 +67,11 @@ def parse():
                     help="measured HBM bytes per launch (rocprofv3 --pmc summary)")
     ap.add_argument("--weights", default="packed", choices=["packed", "rows"],
                     help="expert weight layout: packed once at layer construction (default) or row-major")
+    ap.add_argument("--graph", action="store_true",
+                    help="MoE workloads: capture one layer call in a HIP graph and time its replays")
+    ap.add_argument("--rotate-mb", type=int, default=512,
+                    help="dense workloads: rotate over copies of A and B totalling at least this many MB "
+                         "so that no launch finds its operands in L2/MALL (0: one copy)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (counter calibration)")
     ap.add_argument("--summarize-profile", metavar="DIR", default=None,
@@ -494,10 +499,22 @@ def dense_main(args):
         b_q, sb = hkmoe.quant_tensor(b)
     del a, b
     c = torch.empty((M, N), dtype=torch.float32 if cfg["out"] == "f32" else torch.bfloat16, device=dev)
+    # The reference times rotating input buffers (4_wave.cu:517-571): copies of
+    # the operands at distinct addresses, used in turn, so no launch finds its
+    # A and B in L2/MALL from the launch before.
+    opnd_mb = (M + N) * K / 2**20
+    n_rot = max(1, -(-args.rotate_mb // max(1, int(opnd_mb)))) if args.rotate_mb > 0 else 1
     if cfg["mx"]:
-        step = lambda: tk_kernel.dispatch_gemm_mx(a_q, pa, b_q, pb, c)
+        ops = [(a_q, pa, b_q, pb)] + [(a_q.clone(), pa.clone(), b_q.clone(), pb.clone()) for _ in range(n_rot - 1)]
+        run = lambda o: tk_kernel.dispatch_gemm_mx(o[0], o[1], o[2], o[3], c)
     else:
-        step = lambda: tk_kernel.dispatch_gemm_fp8(a_q, b_q, c, sa, sb)
+        ops = [(a_q, b_q, sa, sb)] + [(a_q.clone(), b_q.clone(), sa.clone(), sb.clone()) for _ in range(n_rot - 1)]
+        run = lambda o: tk_kernel.dispatch_gemm_fp8(o[0], o[1], c, o[2], o[3])
+    it = [0]
+
+    def step():
+        run(ops[it[0] % n_rot])
+        it[0] += 1
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -532,7 +549,8 @@ def dense_main(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "e4m3",
         "data": "synthetic (seeded torch normal on device, quantised by the path's quantisers)",
         "config": {"workload": f"{args.config}_gemm", "M": M, "N": N, "K": K,
-                   "scales": "1x32 e8m0 (MX)" if cfg["mx"] else "per-tensor", "out": cfg["out"]},
+                   "scales": "1x32 e8m0 (MX)" if cfg["mx"] else "per-tensor", "out": cfg["out"],
+                   "operand_copies": n_rot},
         "pct_fp8_peak": round(100.0 * value / PEAK_FP8_TFLOPS, 2),
         "roofline": {"bound": "mfma", "kernel": "gemm_mx" if cfg["mx"] else "gemm_fp8",
                      "achieved": round(ach, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
@@ -569,12 +587,25 @@ def main():
         layer = hkmoe.MoELayer(inp["w13_q"], inp["w13_scale"], inp["w2_q"], inp["w2_scale"], inp["top_k"],
                                pack=args.weights == "packed")
     out = torch.empty((cfg["T"], cfg["H"]), dtype=torch.bfloat16, device=dev)
+    step = lambda: layer(inp["x_q"], inp["x_scale"], inp["logits"], out=out)
+    if args.graph:
+        # one eager call sizes the workspace; the captured call is replayed
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        step = graph.replay
     for _ in range(args.warmup):
-        layer(inp["x_q"], inp["x_scale"], inp["logits"], out=out)
+        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        layer(inp["x_q"], inp["x_scale"], inp["logits"], out=out)
+        step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
     flops = gemm_flops(cfg)
@@ -608,7 +639,7 @@ def main():
                    "scales": ("1x32 e8m0 (MX) weights and activations" if cfg.get("mx") else
                               "128x128 weight / 1x128 activation blocks" if cfg["block"] else "per-tensor"),
                    "routing": "zipf(1.1) skew" if cfg["skew"] else "N(0,1) logits",
-                   "weights": args.weights,
+                   "weights": args.weights, "launch": "hip_graph" if args.graph else "eager",
                    "active_experts": int((counts > 0).sum()), "max_rows": int(counts.max())},
         "pct_fp8_peak": round(100.0 * value / PEAK_FP8_TFLOPS, 2),
         "roofline": {"bound": "mfma", "kernel": "grouped_gemm1 (gate/up + SiLU*up)",

@@ -157,12 +157,18 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
     }
   }
   if (act) {
+    // 16 independent loads in flight, then the running sum and the stores
     int run = before;
-    for (int b = b0; b < b1; ++b) {
-      const int64_t i = static_cast<int64_t>(b) * num_experts + e;
-      const int c = block_counts[i];
-      block_base[i] = run;
-      run += c;
+    for (int b = b0; b < b1; b += 16) {
+      int c[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        c[u] = (b + u < b1) ? block_counts[static_cast<int64_t>(b + u) * num_experts + e] : 0;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (b + u < b1) block_base[static_cast<int64_t>(b + u) * num_experts + e] = run;
+        run += c[u];
+      }
     }
   }
   // scan over experts (threads with part == 0 carry the expert totals)
@@ -336,27 +342,43 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
 
 // ---------------------------------------------------------------------------
 // 5. combine: out[t] = bf16(sum_j w[t,j] * y[inv_perm[t*k+j]]), one
-//    workgroup per token, 8 columns (16 bytes) per thread and step.
+//    workgroup per token, 8 columns (16 bytes) per thread and step.  The
+//    token's weights and y rows are staged in LDS once; the y loads of up to
+//    8 slots are issued together, then summed in slot order j = 0 .. k-1.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const float* __restrict__ topk_w,
                                                       const int32_t* __restrict__ inv_perm,
                                                       int top_k, int hidden,
                                                       uint16_t* __restrict__ out) {
+  __shared__ float s_w[kMaxTopK];
+  __shared__ int32_t s_row[kMaxTopK];
   const int64_t t = blockIdx.x;
+  if (threadIdx.x < top_k) {
+    s_w[threadIdx.x] = topk_w[t * top_k + threadIdx.x];
+    s_row[threadIdx.x] = inv_perm[t * top_k + threadIdx.x];
+  }
+  __syncthreads();
   const int cols8 = hidden / 8;
   for (int c = threadIdx.x; c < cols8; c += 256) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < top_k; ++j) {
-      const int64_t f = t * top_k + j;
-      const float w = topk_w[f];
-      const int64_t p = inv_perm[f];
-      const uint4 v = *reinterpret_cast<const uint4*>(y + p * hidden + c * 8);
-      const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+    for (int j0 = 0; j0 < top_k; j0 += 8) {
+      uint4 v[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        acc[2 * u] = acc[2 * u] + w * bf16_bits_to_f32(wv[u] & 0xffffu);
-        acc[2 * u + 1] = acc[2 * u + 1] + w * bf16_bits_to_f32(wv[u] >> 16);
+      for (int u = 0; u < 8; ++u)
+        if (j0 + u < top_k)
+          v[u] = *reinterpret_cast<const uint4*>(y + static_cast<int64_t>(s_row[j0 + u]) * hidden + c * 8);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (j0 + u < top_k) {
+          const float w = s_w[j0 + u];
+          const uint32_t wv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[2 * q] = acc[2 * q] + w * bf16_bits_to_f32(wv[q] & 0xffffu);
+            acc[2 * q + 1] = acc[2 * q + 1] + w * bf16_bits_to_f32(wv[q] >> 16);
+          }
+        }
       }
     }
     uint4 o;
