@@ -15,7 +15,11 @@
 
 #include "../../include/hkmoe.h"
 #include "gemm_fp8.hpp"
+#include "gemm_narrow.hpp"
 #include "moe_kernels.hpp"
+
+#include <cstdlib>
+#include <mutex>
 
 using namespace hkmoe;
 
@@ -66,8 +70,18 @@ int device_cus() {
   return cus[dev];
 }
 
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+int route_blocks(int64_t t) { return static_cast<int>((t + kRouteTok - 1) / kRouteTok); }
+
+int pow2_at_least(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
 template <Epi EPI, Scale SC>
-int launch_gemm(GemmParams p, hipStream_t stream) {
+int launch_gemm(GemmParams p, hipStream_t stream, int grid_override = 0) {
   p.a_bytes = static_cast<uint32_t>(std::min<int64_t>(p.a_rows * p.K, 0xffffffffll));
   static bool attr_set[kMaxDevices] = {false};
   int dev = 0;
@@ -79,26 +93,148 @@ int launch_gemm(GemmParams p, hipStream_t stream) {
     if (err != hipSuccess) return fail(HKMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(err));
     attr_set[dev] = true;
   }
-  const int grid = device_cus();
+  const int grid = grid_override > 0 ? grid_override : device_cus();
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), kLdsBytes, stream, p);
   return check_launch("gemm_fp8_persistent");
 }
 
-size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
-
-int route_blocks(int64_t t) { return static_cast<int>((t + kRouteTok - 1) / kRouteTok); }
-
-int pow2_at_least(int v) {
-  int p = 1;
-  while (p < v) p <<= 1;
-  return p;
+// Prefetch depth of the narrow kernel for K / 128 steps: the largest of 8, 4,
+// 2 that divides the step count (0: the narrow path cannot run this K).
+int narrow_depth(int k_steps) {
+  return k_steps % 8 == 0 ? 8 : k_steps % 4 == 0 ? 4 : k_steps % 2 == 0 ? 2 : 0;
 }
+
+template <Epi EPI, int P>
+int launch_narrow_p(const GemmParams& p, hipStream_t stream, int grid) {
+  static bool attr_set[kMaxDevices] = {false};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  auto kern = gemm_fp8_narrow<EPI, P>;
+  constexpr int lds = narrow_lds_bytes(P);
+  if (dev >= 0 && dev < kMaxDevices && !attr_set[dev]) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (err != hipSuccess) return fail(HKMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(err));
+    attr_set[dev] = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, p);
+  return check_launch("gemm_fp8_narrow");
+}
+
+template <Epi EPI>
+int launch_narrow(GemmParams p, hipStream_t stream, int grid) {
+  p.a_bytes = static_cast<uint32_t>(std::min<int64_t>(p.a_rows * p.K, 0xffffffffll));
+  switch (narrow_depth(p.K / kBK)) {
+    case 8: return launch_narrow_p<EPI, 8>(p, stream, grid);
+    case 4: return launch_narrow_p<EPI, 4>(p, stream, grid);
+    case 2: return launch_narrow_p<EPI, 2>(p, stream, grid);
+    default: return fail(HKMOE_ERR_INVALID_ARGUMENT, "narrow GEMM: K=%d has an odd number of 128 steps", p.K);
+  }
+}
+
+// Narrow path settings, read once from the environment:
+//   HKMOE_NARROW_CUS   workgroups (CUs) of the narrow kernels, 0 = off (default 48)
+//   HKMOE_NARROW_MAX   largest expert (rows) the narrow kernel takes, <= 64 (default 64)
+//   HKMOE_NARROW_SHARE 1: the first wide GEMM leaves those CUs to the narrow
+//                      kernel (grid = CUs - HKMOE_NARROW_CUS); 0: full grid (default 1).
+//                      A full-grid wide GEMM takes every CU first, and the narrow
+//                      kernel then mostly runs after it.
+// hkmoe_set_narrow overrides them.
+struct NarrowConfig {
+  int cus, max_rows, share;
+};
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return (v && *v) ? std::atoi(v) : dflt;
+}
+std::mutex g_narrow_mu;
+NarrowConfig& narrow_config_ref() {
+  static NarrowConfig cfg = [] {
+    NarrowConfig c;
+    c.cus = std::max(0, env_int("HKMOE_NARROW_CUS", 48));
+    c.max_rows = std::min(kNarrowRows, std::max(0, env_int("HKMOE_NARROW_MAX", kNarrowRows)));
+    c.share = env_int("HKMOE_NARROW_SHARE", 1) != 0;
+    return c;
+  }();
+  return cfg;
+}
+NarrowConfig narrow_config() {
+  std::lock_guard<std::mutex> g(g_narrow_mu);
+  return narrow_config_ref();
+}
+
+// Per-device auxiliary stream (default priority, non-blocking) and fork/join
+// events of the one-call layer.  Created on the first call that is not being
+// captured into a graph; the mutex keeps fork/join sequences of concurrent
+// host threads from interleaving on the shared events.
+struct AuxStreams {
+  hipStream_t aux = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool ok = false;
+};
+std::mutex g_aux_mu;
+AuxStreams g_aux[kMaxDevices];
+
+int get_aux(hipStream_t main_stream, AuxStreams** out) {
+  *out = nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return HKMOE_OK;
+  AuxStreams& a = g_aux[dev];
+  if (!a.ok) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(main_stream, &st) != hipSuccess || st != hipStreamCaptureStatusNone)
+      return HKMOE_OK;  // no set-up under capture: this call runs without the narrow path
+    if (hipStreamCreateWithFlags(&a.aux, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&a.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&a.join, hipEventDisableTiming) != hipSuccess)
+      return fail(HKMOE_ERR_HIP, "moe_forward: cannot create the auxiliary stream / events");
+    a.ok = true;
+  }
+  *out = &a;
+  return HKMOE_OK;
+}
+
+int launch_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
+                          int32_t* counts, int32_t* offsets, int32_t* block_base,
+                          int32_t* mtile_offsets, int32_t* mtile_list, float* amax_reset,
+                          int32_t* tile_counters, int narrow_max, int32_t* narrow_info,
+                          hipStream_t stream) {
+  const int nblk = route_blocks(num_tokens);
+  const int e_stride = pow2_at_least(num_experts);
+  const int parts = kScanThreads / e_stride;
+  hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(kScanThreads), 0, stream, block_counts, nblk,
+                     num_experts, e_stride, parts, counts, offsets, block_base, mtile_offsets,
+                     mtile_list, kBM, amax_reset, tile_counters, narrow_max, narrow_info);
+  return check_launch("expert_offsets_kernel");
+}
+
 
 }  // namespace
 
 extern "C" {
 
 int hkmoe_version(void) { return 200; }
+
+int hkmoe_set_narrow(int32_t cus, int32_t max_rows, int32_t wide_share) {
+  HK_REQUIRE(cus >= 0 && cus <= 4096, "set_narrow: cus=%d outside [0, 4096]", cus);
+  HK_REQUIRE(max_rows >= 0 && max_rows <= kNarrowRows, "set_narrow: max_rows=%d outside [0, %d]", max_rows,
+             kNarrowRows);
+  std::lock_guard<std::mutex> g(g_narrow_mu);
+  NarrowConfig& c = narrow_config_ref();
+  c.cus = cus;
+  c.max_rows = max_rows;
+  c.share = wide_share != 0;
+  return HKMOE_OK;
+}
+
+int hkmoe_get_narrow(int32_t* cus, int32_t* max_rows, int32_t* wide_share) {
+  HK_REQUIRE(cus && max_rows && wide_share, "get_narrow: null pointer");
+  const NarrowConfig c = narrow_config();
+  *cus = c.cus;
+  *max_rows = c.max_rows;
+  *wide_share = c.share;
+  return HKMOE_OK;
+}
 
 const char* hkmoe_last_error(void) { return g_last_error.c_str(); }
 
@@ -163,14 +299,9 @@ int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_
              num_experts, kMaxExperts);
   HK_REQUIRE(num_tokens >= 0, "expert_offsets: bad T");
   HK_REQUIRE(num_tokens == 0 || block_counts, "expert_offsets: null block_counts");
-  const int nblk = route_blocks(num_tokens);
-  const int e_stride = pow2_at_least(num_experts);
-  const int parts = kScanThreads / e_stride;
-  hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(kScanThreads), 0,
-                     static_cast<hipStream_t>(stream), block_counts, nblk, num_experts, e_stride,
-                     parts, counts, offsets, block_base, mtile_offsets, mtile_list, kBM, amax_reset,
-                     tile_counters);
-  return check_launch("expert_offsets_kernel");
+  return launch_expert_offsets(block_counts, num_tokens, num_experts, counts, offsets, block_base,
+                               mtile_offsets, mtile_list, amax_reset, tile_counters, 0, nullptr,
+                               static_cast<hipStream_t>(stream));
 }
 
 int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_experts, int32_t top_k,
@@ -203,13 +334,16 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
   return check_launch("scatter_kernel");
 }
 
-int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gather,
-                        int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
-                        const int32_t* offsets, const int32_t* mtile_offsets,
-                        const int32_t* mtile_list, int64_t rows,
-                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
-                        int w_layout, int out_format, void* h, float* h_aux,
-                        int32_t* tile_counters, hkmoe_stream_t stream) {
+// narrow_cnt: skip (wide kernel) the list's last *narrow_cnt M tiles; narrow_grid > 0:
+// run the narrow kernel on exactly those tiles instead, with that many workgroups.
+static int grouped_gemm1_impl(const void* x, const float* x_scale, const int32_t* gather,
+                              int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
+                              const int32_t* offsets, const int32_t* mtile_offsets,
+                              const int32_t* mtile_list, int64_t rows,
+                              int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
+                              int w_layout, int out_format, void* h, float* h_aux,
+                              int32_t* tile_counters, hkmoe_stream_t stream,
+                              const int32_t* narrow_cnt, int wide_grid, int narrow_grid) {
   HK_REQUIRE(x && w13 && offsets && mtile_offsets && h, "grouped_gemm1: null pointer");
   HK_REQUIRE(x_scale && w13_scale, "grouped_gemm1: null scale pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1: bad E=%d", num_experts);
@@ -253,16 +387,37 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
   p.mtile_list = mtile_list;
   p.blk_m_log2 = 1;  // 2 x 16 tile blocks
   p.tile_ctr = tile_counters;
+  p.narrow_cnt = narrow_cnt;
   auto s = static_cast<hipStream_t>(stream);
+  if (narrow_grid > 0) {
+    if (scale_mode != HKMOE_SCALE_BLOCK || out_format != HKMOE_E4M3 || narrow_cnt == nullptr ||
+        mtile_list == nullptr)
+      return fail(HKMOE_ERR_INVALID_ARGUMENT, "grouped_gemm1: the narrow kernel needs block scales, "
+                                              "e4m3 output and the M-tile list");
+    p.c_scale = h_aux;
+    return launch_narrow<Epi::kSiluQuant>(p, s, narrow_grid);
+  }
   if (scale_mode == HKMOE_SCALE_TENSOR) {
     p.amax = h_aux;
-    return launch_gemm<Epi::kSiluBf16, Scale::kTensor>(p, s);
+    return launch_gemm<Epi::kSiluBf16, Scale::kTensor>(p, s, wide_grid);
   }
   if (out_format == HKMOE_E4M3) {
     p.c_scale = h_aux;
-    return launch_gemm<Epi::kSiluQuant, Scale::kBlock>(p, s);
+    return launch_gemm<Epi::kSiluQuant, Scale::kBlock>(p, s, wide_grid);
   }
-  return launch_gemm<Epi::kSiluBf16, Scale::kBlock>(p, s);
+  return launch_gemm<Epi::kSiluBf16, Scale::kBlock>(p, s, wide_grid);
+}
+
+int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gather,
+                        int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
+                        const int32_t* offsets, const int32_t* mtile_offsets,
+                        const int32_t* mtile_list, int64_t rows,
+                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
+                        int w_layout, int out_format, void* h, float* h_aux,
+                        int32_t* tile_counters, hkmoe_stream_t stream) {
+  return grouped_gemm1_impl(x, x_scale, gather, gather_div, x_rows, w13, w13_scale, offsets,
+                            mtile_offsets, mtile_list, rows, num_experts, hidden, inter, scale_mode,
+                            w_layout, out_format, h, h_aux, tile_counters, stream, nullptr, 0, 0);
 }
 
 int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, const float* amax,
@@ -287,11 +442,12 @@ int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, co
   return check_launch("requant_tensor_kernel");
 }
 
-int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
-                        const int32_t* offsets, const int32_t* mtile_offsets,
-                        const int32_t* mtile_list, int64_t rows,
-                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
-                        int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream) {
+static int grouped_gemm2_impl(const void* hq, const float* hs, const void* w2, const float* w2_scale,
+                              const int32_t* offsets, const int32_t* mtile_offsets,
+                              const int32_t* mtile_list, int64_t rows,
+                              int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
+                              int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream,
+                              const int32_t* narrow_cnt, int wide_grid, int narrow_grid) {
   HK_REQUIRE(hq && hs && w2 && w2_scale && offsets && mtile_offsets && y, "grouped_gemm2: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2: hidden=%d must be a multiple of 256", hidden);
@@ -325,9 +481,25 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
   p.mtile_list = mtile_list;
   p.blk_m_log2 = 1;  // 2 x 16 tile blocks
   p.tile_ctr = tile_counters;
+  p.narrow_cnt = narrow_cnt;
   auto s = static_cast<hipStream_t>(stream);
-  return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kStoreBf16, Scale::kBlock>(p, s)
-                                         : launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s);
+  if (narrow_grid > 0) {
+    if (scale_mode != HKMOE_SCALE_BLOCK || narrow_cnt == nullptr || mtile_list == nullptr)
+      return fail(HKMOE_ERR_INVALID_ARGUMENT, "grouped_gemm2: the narrow kernel needs block scales "
+                                              "and the M-tile list");
+    return launch_narrow<Epi::kStoreBf16>(p, s, narrow_grid);
+  }
+  return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kStoreBf16, Scale::kBlock>(p, s, wide_grid)
+                                         : launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s, wide_grid);
+}
+
+int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
+                        const int32_t* offsets, const int32_t* mtile_offsets,
+                        const int32_t* mtile_list, int64_t rows,
+                        int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
+                        int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream) {
+  return grouped_gemm2_impl(hq, hs, w2, w2_scale, offsets, mtile_offsets, mtile_list, rows, num_experts,
+                            hidden, inter, scale_mode, w_layout, y, tile_counters, stream, nullptr, 0, 0);
 }
 
 int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k, int32_t gate_up,
@@ -377,6 +549,7 @@ struct MoeWorkspace {
   int32_t* mtile_list;  // [M tiles][2], at most ceil(T*k/256) + E tiles
   float* amax;
   int32_t* tile_ctr;  // HKMOE_TILE_COUNTERS
+  int32_t* narrow_info;  // [0] narrow M tiles, [1] / [2] narrow item counters of GEMM 1 / 2
   int32_t* perm;
   int32_t* inv_perm;
   uint16_t* h;   // per-tensor mode only: bf16 intermediate before requantisation
@@ -413,6 +586,7 @@ MoeWorkspace carve(uint8_t* base, int64_t t, int32_t e, int32_t k, int32_t hidde
   w.mtile_list = reinterpret_cast<int32_t*>(take(((r + kBM - 1) / kBM + e) * 8));
   w.amax = reinterpret_cast<float*>(take(4));
   w.tile_ctr = reinterpret_cast<int32_t*>(take(HKMOE_TILE_COUNTERS * 4));
+  w.narrow_info = reinterpret_cast<int32_t*>(take((1 + kNarrowCounters) * 4));
   w.perm = reinterpret_cast<int32_t*>(take(r * 4));
   w.inv_perm = reinterpret_cast<int32_t*>(take(r * 4));
   const int64_t ws = mx_words_per_step(r, e);
@@ -462,13 +636,53 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
   const MoeWorkspace w = carve(static_cast<uint8_t*>(workspace), num_tokens, num_experts, top_k,
                                hidden, inter, scale_mode);
   const int64_t rows = num_tokens * top_k;
+  auto s = static_cast<hipStream_t>(stream);
+  // Narrow path (block scales): experts of at most HKMOE_NARROW_MAX rows go to
+  // the weight-streaming narrow kernels on an auxiliary stream, which run
+  // beside the 256x256 kernels of the larger experts on the main stream.
+  const NarrowConfig nc = narrow_config();
+  AuxStreams* aux = nullptr;
+  if (block && nc.cus > 0 && nc.max_rows > 0 && narrow_depth(hidden / kBK) > 0 &&
+      narrow_depth(inter / kBK) > 0)
+    HK_TRY(get_aux(s, &aux));
+  std::unique_lock<std::mutex> aux_lock(g_aux_mu, std::defer_lock);
+  if (aux) aux_lock.lock();
   HK_TRY(hkmoe_route_topk(logits, num_tokens, num_experts, top_k, w.topk_idx, w.topk_w,
                           w.block_counts, stream));
-  HK_TRY(hkmoe_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets,
-                              w.block_base, w.mtile_offsets, w.mtile_list, w.amax, w.tile_ctr,
-                              stream));
+  HK_TRY(launch_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets,
+                               w.block_base, w.mtile_offsets, w.mtile_list, w.amax, w.tile_ctr,
+                               aux ? nc.max_rows : 0, aux ? w.narrow_info : nullptr, s));
   HK_TRY(hkmoe_scatter(w.topk_idx, num_tokens, num_experts, top_k, w.offsets, w.block_base, w.perm,
                        w.inv_perm, nullptr, nullptr, hidden, scale_mode, nullptr, nullptr, stream));
+  if (aux) {
+    // fork: both GEMMs of the narrow experts on the auxiliary stream, enqueued
+    // first so that their workgroups find free CUs; join before the combine
+    const int ncus = std::min(nc.cus, device_cus());
+    if (hipEventRecord(aux->fork, s) != hipSuccess || hipStreamWaitEvent(aux->aux, aux->fork, 0) != hipSuccess)
+      return fail(HKMOE_ERR_HIP, "moe_forward: fork to the auxiliary stream failed");
+    HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
+                              w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
+                              w_layout, HKMOE_E4M3, w.hq, w.hs, w.narrow_info + 1, aux->aux,
+                              w.narrow_info, 0, ncus));
+    HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
+                              num_experts, hidden, inter, scale_mode, w_layout, w.y, w.narrow_info + 2,
+                              aux->aux, w.narrow_info, 0, ncus));
+    if (hipEventRecord(aux->join, aux->aux) != hipSuccess)
+      return fail(HKMOE_ERR_HIP, "moe_forward: join event failed");
+    const int wide_grid = nc.share ? std::max(1, device_cus() - ncus) : 0;
+    HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
+                              w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
+                              w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream, w.narrow_info,
+                              wide_grid, 0));
+    HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
+                              num_experts, hidden, inter, scale_mode, w_layout, w.y, w.tile_ctr + 8,
+                              stream, w.narrow_info, 0, 0));
+    if (hipStreamWaitEvent(s, aux->join, 0) != hipSuccess)
+      return fail(HKMOE_ERR_HIP, "moe_forward: join of the auxiliary stream failed");
+    aux_lock.unlock();
+    HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
+    return HKMOE_OK;
+  }
   if (block) {
     // GEMM 1 reads token rows through perm and writes the requantised e4m3
     // intermediate and its 1x128 group scales directly.

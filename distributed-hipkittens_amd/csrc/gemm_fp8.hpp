@@ -95,6 +95,9 @@ struct GemmParams {
   const int32_t* mtile_list;   // optional [M tiles][2] = (expert, first row), in schedule order
   float* amax;                 // kSiluBf16: running max |h| (uint-ordered), may be null
   int32_t* tile_ctr;           // optional: 8 zeroed per-XCD tile counters (dynamic schedule)
+                               // (narrow kernel: one zeroed item counter)
+  const int32_t* narrow_cnt;   // optional: the last *narrow_cnt M-tile list entries belong to
+                               // the narrow kernel (gemm_narrow.hpp); this kernel skips them
   int64_t rows;                // output rows (dense: M)
   int64_t a_rows;              // rows addressable through `a`
   int64_t as_rs, as_ks;        // activation scale strides (row, K block)
@@ -232,7 +235,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 
   const bool dense = (p.offsets == nullptr);
   const int total_mtiles = dense ? static_cast<int>((p.rows + kBM - 1) / kBM)
-                                 : __builtin_amdgcn_readfirstlane(p.mtile_offsets[p.num_experts]);
+                                 : __builtin_amdgcn_readfirstlane(p.mtile_offsets[p.num_experts] -
+                                                                  (p.narrow_cnt ? *p.narrow_cnt : 0));
   const int k_steps = p.K / kBK;
 
   // XCD-aware virtual id: workgroups are dispatched round-robin over 8 XCDs,
@@ -328,6 +332,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     // kt*128.  Packed weights: the tile's K step kt is the 32 KiB stage image
     // at kt*32 KiB of the tile's own panel, so instruction i of wave wg reads
     // the 1 KiB at (32*i + 8*wg)*128 linearly.
+    // Lane offsets of the two register halves of a B fragment within its
+    // 2 KiB of the stage: fragment-major (packed weights) or swizzled rows,
+    // in the K order of the MFMA variant (read_frag / read_frag_mx).
+    int b_lo, b_hi;
+    if (p.b_packed) {
+      if constexpr (kMX) {
+        b_lo = (lg & 1) * 1024 + ((lg >> 1) * 16 + l16) * 16;
+        b_hi = (lg & 1) * 1024 + (((lg >> 1) + 2) * 16 + l16) * 16;
+      } else {
+        b_lo = lane * 16;
+        b_hi = 1024 + lane * 16;
+      }
+    } else {
+      b_lo = l16 * kBK + ((kMX ? lg : 2 * lg) ^ fx) * 16;
+      b_hi = l16 * kBK + ((kMX ? lg + 4 : 2 * lg + 1) ^ fx) * 16;
+    }
     i32x4 b_srd;
     int b_voff, b_kstride;
     if (p.b_packed) {
@@ -483,7 +503,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       i32x8 bf[4], af[4];
       int mx_sb = 0, mx_sa0 = 0, mx_sa1 = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = read_operand<kMX>(sb, wg * 64 + j * 16 + l16, lg, fx);
+      for (int j = 0; j < 4; ++j) {
+        const uint8_t* fb = sb + (wg * 4 + j) * 2048;
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(fb + b_lo);
+        const i32x4 hi = *reinterpret_cast<const i32x4*>(fb + b_hi);
+        bf[j].s0 = lo.x; bf[j].s1 = lo.y; bf[j].s2 = lo.z; bf[j].s3 = lo.w;
+        bf[j].s4 = hi.x; bf[j].s5 = hi.y; bf[j].s6 = hi.z; bf[j].s7 = hi.w;
+      }
       if constexpr (kMX) {
         // exponent words: B rows wg*64 + 16j + l16 (byte j), A rows of
         // sub-tiles 0-3 and 4-7 (byte i % 4), all for K block 4kt + lg
@@ -754,12 +780,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 
 // Packed weight layout (a load-time transform; the grouped GEMMs then stream
 // every weight panel sequentially instead of 128 bytes from each of 256 rows
-// 7-14 KiB apart): for expert e, 256-row N tile nt and K step kt,
-//   packed[((e*(nb/256) + nt)*(K/128) + kt)*32 KiB + R*128 + P*16 + b]
-//     = w[e][wrow(R)][kt*128 + (P ^ swz(R))*16 + b],
-// i.e. the byte image of the GEMM's B stage.  wrow(R) = nt*256 + R, or with
-// gate_up = I (fused gate/up weights [gate I rows | up I rows]) the 64-row
-// quarter R>>6 holds 32 gate rows then the 32 matching up rows:
+// 7-14 KiB apart).  For expert e, 256-row N tile nt and K step kt the 32 KiB
+// block at ((e*(nb/256) + nt)*(K/128) + kt)*32 KiB holds the tile's sixteen
+// 16-row MFMA fragments in operand-register order ("fragment-major"):
+//   block[f*2048 + h*1024 + l*16 + b] = w[e][wrow(16f + l%16)][kt*128 + (2*(l/16) + h)*16 + b],
+// i.e. lane l's registers 0-3 (h = 0) and 4-7 (h = 1) of fragment f, so one
+// 64-lane 16-byte load of 1 KiB contiguous bytes fills one register half of a
+// fragment (the narrow kernel), and the 256x256 kernel copies the block
+// linearly into LDS and reads each fragment half as 64 consecutive 16-byte
+// chunks.  wrow(R) = nt*256 + R, or with gate_up = I (fused gate/up weights
+// [gate I rows | up I rows]) the 64-row quarter R>>6 holds 32 gate rows then
+// the 32 matching up rows:
 //   wrow(R) = nt*128 + 32*(R>>6) + (R&31) + ((R>>5)&1)*I.
 // One thread moves one 16-byte chunk; writes are linear.
 __global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __restrict__ w, int64_t nb,
@@ -769,16 +800,18 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __rest
   const int64_t ntile = nb / kBN;
   for (int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < chunks;
        c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t blk = c >> 11;  // 2048 chunks per 32 KiB stage image
+    const int64_t blk = c >> 11;  // 2048 chunks per 32 KiB block
     const int in = static_cast<int>(c & 2047);
-    const int R = in >> 3, P = in & 7;
+    const int f = in >> 7, h = (in >> 6) & 1, l = in & 63;
+    const int R = 16 * f + (l & 15);
+    const int chunk = 2 * (l >> 4) + h;
     const int kt = static_cast<int>(blk % ks);
     const int64_t tile = blk / ks;
     const int64_t e = tile / ntile;
     const int nt = static_cast<int>(tile - e * ntile);
     const int64_t wrow = gate_up ? nt * 128 + 32 * (R >> 6) + (R & 31) + ((R >> 5) & 1) * gate_up
                                  : static_cast<int64_t>(nt) * kBN + R;
-    const uint8_t* src = w + (e * nb + wrow) * K + kt * kBK + ((P ^ swz(R)) << 4);
+    const uint8_t* src = w + (e * nb + wrow) * K + kt * kBK + (chunk << 4);
     *reinterpret_cast<uint4*>(out + (c << 4)) = *reinterpret_cast<const uint4*>(src);
   }
 }

@@ -1,0 +1,479 @@
+// Narrow grouped GEMM for small expert segments (at most 64 rows), block
+// scales, gfx950.
+//
+// A segment of <= 64 rows against a 256-row weight panel does 2*64*256*K
+// FLOPs for 256*K weight bytes: it is bound by streaming the weights from HBM,
+// not by the MFMA.  The 256x256 persistent kernel (gemm_fp8.hpp) keeps only
+// two K steps of weights in flight per CU and needs the whole CU's LDS for
+// them, so such tiles run at HBM latency.  This kernel streams the weights
+// straight into VGPRs instead, P K steps ahead (P * 4 KiB per wave, 256 KiB
+// per CU at P = 8), so a few dozen CUs can pull HBM bandwidth while the other
+// CUs run the compute-bound 256x256 tiles of the large experts (the host
+// launches the two kernels on two streams).
+//
+//  * work item: (narrow segment m, 256-row N tile nt); workgroup b takes items
+//    b, b + grid, b + 2*grid, ... (items cost nearly the same).  Segment m is
+//    entry first + m of the M-tile list (the narrow experts are listed last).
+//  * 8 waves; wave w owns 32 weight rows = two 16-row fragments:
+//      gate/up GEMM: gate rows 16w..16w+15 of the tile's 128 and the matching
+//                    up rows (h columns 16w..16w+15);
+//      plain GEMM:   rows 32w..32w+31 of the 256.
+//    Each lane loads its fragment rows' 32 K bytes per step with two 16-byte
+//    buffer loads per fragment, in the register order read_frag produces from
+//    LDS: the MFMA operands, the rescale arithmetic and the epilogue are those
+//    of the 256x256 kernel, so both kernels give the same bits.
+//  * activations: every wave DMAs 8 of the segment's 64 rows (rows past the
+//    segment repeat its last row) into an LDS ring of P+1 stages, and its own
+//    copy of the 64 row scales and of its two weight scales (all lanes active,
+//    so the compiler counts every load), loaded P steps ahead like the
+//    weights; one barrier per K step.
+//  * every wave issues exactly 7 vector-memory instructions per K step (A rows,
+//    A scales, weight scales, 4 weight loads), so "step kt has landed" is
+//    vmcnt(7*(P-1)); after the last item the loads continue on that item's
+//    first steps (valid addresses, never read), so the count never changes.
+//  * K steps per item must be a multiple of P, so a group of P unrolled steps
+//    never straddles two items; the loads of an item's last group are the next
+//    item's first P steps.
+//  * the compiler must not wait for the prefetch window by itself: LDS
+//    accesses and the item decode's scalar loads are inline asm with their own
+//    lgkmcnt waits (it would otherwise wait for every buffer->LDS DMA before an
+//    LDS access, and for pending stores before a scalar load), and the next
+//    item's gathered row indices reach LDS by a DMA issued a group before they
+//    are read.
+#pragma once
+
+#include "gemm_fp8.hpp"
+
+namespace hkmoe {
+
+constexpr int kNarrowRows = 64;
+constexpr int kNarrowAStage = kNarrowRows * kBK;                  // 8 KiB of A rows
+constexpr int kNarrowAScale = kNarrowAStage;                      // per wave: the 64 row scales
+constexpr int kNarrowWScale = kNarrowAScale + 8 * 256;             // per wave: its 2 weight scales
+constexpr int kNarrowStage = kNarrowWScale + 8 * 256;
+constexpr int kNarrowCtLd = 128 + 8;                              // staged h row (bf16)
+constexpr int kNarrowVmPerStep = 7;
+
+constexpr int narrow_lds_bytes(int P) {
+  // ring, h staging tile, per-wave gathered row indices
+  return (P + 1) * kNarrowStage + kNarrowRows * kNarrowCtLd * 2 + 8 * 256;
+}
+static_assert(narrow_lds_bytes(8) <= 160 * 1024, "LDS budget");
+
+extern "C" __device__ i32x4 hk_raw_buffer_load_v4i32(i32x4 rsrc, int voffset, int soffset,
+                                                     int aux) __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+
+// a[idx] for a wave-uniform idx through the scalar cache, complete on return.
+// Only for data written before the kernel started.
+__device__ __forceinline__ int sload_i32(const int32_t* a, int idx) {
+  const i32x4 srd = make_srd(a, 0xffffffffu);
+  const int off = __builtin_amdgcn_readfirstlane(idx * 4);
+  int v;
+  asm volatile("s_buffer_load_dword %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=&s"(v) : "s"(srd), "s"(off));
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// LDS accesses of the narrow kernel are written as inline asm with their own
+// lgkmcnt waits; outputs are early-clobber ("=&"), since a load's destination
+// is written after later instructions of the same block have read their
+// address registers.  The compiler cannot tell the ring slots apart, so before any
+// LDS access it can see it would wait for every buffer->LDS DMA still in
+// flight, i.e. for the whole prefetch window.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// One A fragment (two 16-byte chunks at a_lo / a_hi + OFF) and its row scale
+// (a_sc + SOFF), complete on return.
+template <int OFF, int SOFF>
+__device__ __forceinline__ void lds_frag(uint32_t a_lo, uint32_t a_hi, uint32_t a_sc, i32x8& f, float& sc) {
+  i32x4 lo, hi;
+  asm volatile(
+      "ds_read_b128 %0, %3 offset:%6\n\t"
+      "ds_read_b128 %1, %4 offset:%6\n\t"
+      "ds_read_b32 %2, %5 offset:%7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(lo), "=&v"(hi), "=&v"(sc)
+      : "v"(a_lo), "v"(a_hi), "v"(a_sc), "i"(OFF), "i"(SOFF));
+  f.lo = lo;
+  f.hi = hi;
+}
+
+__device__ __forceinline__ float2 lds_read_f2(uint32_t a) {
+  float2 v;
+  asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
+  return v;
+}
+
+__device__ __forceinline__ int lds_read_i32(uint32_t a) {
+  int v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
+  return v;
+}
+
+__device__ __forceinline__ void lds_write_b64(uint32_t a, uint2 v) {
+  asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+
+// 64 bf16 (128 bytes) at a, complete on return
+__device__ __forceinline__ void lds_read_128B(uint32_t a, uint4 (&v)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %8 offset:16\n\t"
+      "ds_read_b128 %2, %8 offset:32\n\t"
+      "ds_read_b128 %3, %8 offset:48\n\t"
+      "ds_read_b128 %4, %8 offset:64\n\t"
+      "ds_read_b128 %5, %8 offset:80\n\t"
+      "ds_read_b128 %6, %8 offset:96\n\t"
+      "ds_read_b128 %7, %8 offset:112\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
+      : "v"(a));
+}
+
+// LDS writes done, then the workgroup barrier (no vmcnt: DMA stays in flight)
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <Epi EPI, int P>
+__global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
+  static_assert(EPI == Epi::kSiluQuant || EPI == Epi::kStoreBf16, "narrow epilogues");
+  static_assert(P == 2 || P == 4 || P == 8, "prefetch depth");
+  static_assert(kNarrowVmPerStep * (P - 1) <= 63, "vmcnt range");
+  constexpr bool kSilu = (EPI == Epi::kSiluQuant);
+  constexpr int kRing = P + 1;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  uint16_t* ct = reinterpret_cast<uint16_t*>(smem + kRing * kNarrowStage);
+  int32_t* gidx = reinterpret_cast<int32_t*>(smem + kRing * kNarrowStage + kNarrowRows * kNarrowCtLd * 2);
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+  const int fx = swz(l16);
+
+  const int k_steps = p.K / kBK;
+  const int groups = k_steps / P;
+  const int total_mt = sload_i32(p.mtile_offsets, p.num_experts);
+  const int n_narrow = sload_i32(p.narrow_cnt, 0);
+  const int first = total_mt - n_narrow;
+  const int n_items = n_narrow * p.n_tiles;
+  const int grid = gridDim.x;
+  if (static_cast<int>(blockIdx.x) >= n_items) return;
+
+  // this wave's two fragment rows, tile-local (row R of the 256-row tile;
+  // fragment R/16 of the packed block) and relative to the N tile's first
+  // weight row
+  int frag_r[2], frag_w[2];
+  if constexpr (kSilu) {
+    frag_r[0] = 64 * (wave >> 1) + 16 * (wave & 1) + l16;  // gate row 16w + l16 of the tile
+    frag_r[1] = frag_r[0] + 32;                             // its up row
+    frag_w[0] = 16 * wave + l16;                            // + nt*128
+    frag_w[1] = 16 * wave + l16 + p.n_out;                  // + nt*128 (up half starts at I)
+  } else {
+    frag_r[0] = 32 * wave + l16;
+    frag_r[1] = 32 * wave + 16 + l16;
+    frag_w[0] = frag_r[0];                                  // + nt*256
+    frag_w[1] = frag_r[1];
+  }
+  const int ld_row = 8 * wave + (lane >> 3);                // A row this lane DMAs
+  const int ld_chunk = (lane & 7) ^ swz(ld_row);
+  const i32x4 a_srd = make_srd(p.a, p.a_bytes);
+  const i32x4 as_srd = make_srd(p.a_scale, 0xffffffffu);
+  const i32x4 g_srd = make_srd(p.a_gather, 0xffffffffu);
+  const int64_t kb_per_expert = static_cast<int64_t>(p.nb / kGroup) * k_steps;
+
+  // Lane-constant weight offsets within a K step: packed layout, the two
+  // contiguous 1 KiB register halves of the fragment (one load each, whole
+  // 128-byte lines); row-major, the weight row (relative to the item's first
+  // row, which goes into the descriptor).
+  int wvoff[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (p.b_packed) {
+      // fragment-major block: fragment f's register halves are 1 KiB each
+      const int f = frag_r[j] >> 4;
+      wvoff[2 * j] = (2 * f) * 1024 + lane * 16;
+      wvoff[2 * j + 1] = (2 * f + 1) * 1024 + lane * 16;
+    } else {
+      wvoff[2 * j] = frag_w[j] * p.K + (2 * lg) * 16;
+      wvoff[2 * j + 1] = frag_w[j] * p.K + (2 * lg + 1) * 16;
+    }
+  }
+  // lane-constant LDS offsets within a ring stage: A fragment chunks of row
+  // l16 (fragment i adds 2 KiB), its row scale (fragment i adds 64 bytes), and
+  // this wave's two weight scales
+  const uint32_t smem_base = lds_addr(smem);
+  const uint32_t lo_off = l16 * kBK + (((2 * lg) ^ fx) << 4);
+  const uint32_t hi_off = l16 * kBK + (((2 * lg + 1) ^ fx) << 4);
+  const uint32_t sa_off = kNarrowAScale + 256 * wave + l16 * 4;
+  const uint32_t sb_off = kNarrowWScale + 256 * wave;
+  const uint32_t gidx_wave = lds_addr(gidx) + 256 * wave;
+
+  // weight-scale DMA: lane 0 the first (gate) block row, the other lanes the
+  // second (up) block row of this wave's columns, at K block kt
+  const int ws_voff = (kSilu && lane >= 1) ? (p.n_out / kGroup) * k_steps * 4 : 0;
+  const int kstride = p.b_packed ? kTileBytes : kBK;
+
+  // per-item state of the load side: uniform descriptors, and the lane's
+  // A-row and A-scale offsets
+  struct Load {
+    i32x4 wsrd, ssrd;
+    int a_voff, as_voff;
+  };
+  // per-item state of the compute side
+  struct Item {
+    int row0, valid, nt, mf;
+  };
+
+  // uniform part of item `it` (scalar loads); with a row gather, the DMA of
+  // the segment's 64 gathered row indices into this wave's LDS slot
+  auto decode_head = [&](int it, Load& L, Item& C) {
+    const int m = it / p.n_tiles;
+    const int nt = it - m * p.n_tiles;
+    const int entry = first + m;
+    const int e = sload_i32(p.mtile_list, 2 * entry);
+    const int row0 = sload_i32(p.mtile_list, 2 * entry + 1);
+    const int valid = min(kNarrowRows, sload_i32(p.offsets, e + 1) - row0);
+    C.row0 = row0;
+    C.valid = valid;
+    C.nt = nt;
+    C.mf = (valid + 15) >> 4;
+    if (p.b_packed) {
+      L.wsrd = make_srd(p.b + (static_cast<int64_t>(e) * (p.nb / kBN) + nt) * kBN * p.K,
+                        static_cast<uint32_t>(kBN) * p.K);
+    } else {
+      const int nbase = kSilu ? nt * 128 : nt * kBN;
+      L.wsrd = make_srd(p.b + (static_cast<int64_t>(e) * p.nb + nbase) * p.K,
+                        static_cast<uint32_t>(p.nb - nbase) * p.K);
+    }
+    const int nb0 = kSilu ? nt : 2 * nt + (wave >> 2);
+    L.ssrd = make_srd(p.b_scale + e * kb_per_expert + static_cast<int64_t>(nb0) * k_steps,
+                      static_cast<uint32_t>((kb_per_expert - static_cast<int64_t>(nb0) * k_steps) * 4));
+    if (p.a_gather) load_lds_4B(g_srd, gidx + 64 * wave, (row0 + min(lane, valid - 1)) * 4, 0);
+  };
+  // lane offsets of item C, once its gathered row indices are in LDS
+  auto decode_tail = [&](Load& L, const Item& C) {
+    const int ra = min(ld_row, C.valid - 1), rs = min(lane, C.valid - 1);
+    int ta = C.row0 + ra, ts = C.row0 + rs;
+    if (p.a_gather) {
+      ta = lds_read_i32(gidx_wave + 4 * ra) / p.gather_div;
+      ts = lds_read_i32(gidx_wave + 4 * rs) / p.gather_div;
+    }
+    L.a_voff = ta * p.K + ld_chunk * 16;
+    L.as_voff = static_cast<int>(ts * p.as_rs) * 4;
+  };
+
+  // the 7 loads of K step kt into ring slot `slot` and weight registers wr
+  auto issue = [&](const Load& L, int kt, int slot, i32x8 (&wr)[2]) {
+    // descriptors and K offsets are wave-uniform: keep them in SGPRs (a
+    // descriptor in VGPRs would turn every load into a waterfall loop)
+    i32x4 srd, ssrd;
+    srd.x = __builtin_amdgcn_readfirstlane(L.wsrd.x);
+    srd.y = __builtin_amdgcn_readfirstlane(L.wsrd.y);
+    srd.z = __builtin_amdgcn_readfirstlane(L.wsrd.z);
+    srd.w = __builtin_amdgcn_readfirstlane(L.wsrd.w);
+    ssrd.x = __builtin_amdgcn_readfirstlane(L.ssrd.x);
+    ssrd.y = __builtin_amdgcn_readfirstlane(L.ssrd.y);
+    ssrd.z = __builtin_amdgcn_readfirstlane(L.ssrd.z);
+    ssrd.w = __builtin_amdgcn_readfirstlane(L.ssrd.w);
+    const int ktu = __builtin_amdgcn_readfirstlane(kt);
+    uint8_t* st = smem + __builtin_amdgcn_readfirstlane(slot) * kNarrowStage;
+    load_lds_16B(a_srd, st + 8 * wave * kBK, L.a_voff, ktu * kBK);
+    load_lds_4B(as_srd, st + kNarrowAScale + 256 * wave, L.as_voff, static_cast<int>(ktu * p.as_ks) * 4);
+    load_lds_4B(ssrd, st + kNarrowWScale + 256 * wave, ws_voff, ktu * 4);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      wr[j].lo = hk_raw_buffer_load_v4i32(srd, wvoff[2 * j], ktu * kstride, 0);
+      wr[j].hi = hk_raw_buffer_load_v4i32(srd, wvoff[2 * j + 1], ktu * kstride, 0);
+    }
+  };
+
+  // ---- first item --------------------------------------------------------
+  int it_cur = blockIdx.x;
+  Load L, Ln;
+  Item C, Cn;
+  decode_head(it_cur, L, C);
+  if (p.a_gather) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // own gather DMA
+  decode_tail(L, C);
+  i32x8 wbuf[P][2];
+#pragma unroll
+  for (int s = 0; s < P; ++s) issue(L, s, s, wbuf[s]);
+
+  // The next item is decoded at the first step of group `dgroup`, at least P
+  // steps before its first loads are issued (in the last group) when an item
+  // has two or more groups; its gathered row indices have landed by then.
+  const int dgroup = groups >= 2 ? groups - 2 : 0;
+  int cp_slot = 0;  // ring slot of the step being computed
+  bool have_next = false;
+
+  while (true) {
+    constexpr int MF = 4;
+    const int mf = C.mf;
+    f32x4 acc[MF][2];
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+      acc[i][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float sa_prev[MF] = {0.f, 0.f, 0.f, 0.f};
+    float sb_prev0 = 0.f, sb_prev1 = 0.f;
+
+    for (int g = 0; g < groups; ++g) {
+      const bool last_group = (g == groups - 1);
+#pragma unroll
+      for (int s = 0; s < P; ++s) {
+        const int kt = g * P + s;
+        // scheduling barriers keep each step's MFMAs and loads inside the step,
+        // so the operands of one step are live at a time
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm_barrier<kNarrowVmPerStep * (P - 1)>();
+        __builtin_amdgcn_sched_barrier(0);
+        if (s == 0 && g == dgroup) {
+          have_next = it_cur + grid < n_items;
+          if (have_next) {
+            decode_head(it_cur + grid, Ln, Cn);
+          } else {
+            Ln = L;
+            Cn = C;
+          }
+        }
+        if (s == 0 && last_group && have_next) {
+          // a single-group item decodes and reads its indices in one step
+          if (groups == 1 && p.a_gather) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          decode_tail(Ln, Cn);
+        }
+        const uint32_t st = smem_base + __builtin_amdgcn_readfirstlane(cp_slot) * kNarrowStage;
+        const float2 sbv = lds_read_f2(st + sb_off);
+        const float sb_cur0 = sbv.x;                   // lane 0's DMA: gate / only block
+        const float sb_cur1 = kSilu ? sbv.y : sbv.x;   // lane 1's DMA: up block
+        // rescale and MFMAs, in the 256x256 kernel's arithmetic
+        const float rb0 = sb_prev0 * __builtin_amdgcn_rcpf(sb_cur0);
+        const float rb1 = sb_prev1 * __builtin_amdgcn_rcpf(sb_cur1);
+        sb_prev0 = sb_cur0;
+        sb_prev1 = sb_cur1;
+        // fragment i (rows 16i..16i+15) only while the segment reaches it
+        auto frag_step = [&](auto i_tag) {
+          constexpr int i = decltype(i_tag)::value;
+          i32x8 af;
+          float sa_cur;
+          lds_frag<2048 * i, 64 * i>(st + lo_off, st + hi_off, st + sa_off, af, sa_cur);
+          const float ra = sa_prev[i] * __builtin_amdgcn_rcpf(sa_cur);
+          const float r0 = ra * rb0, r1 = ra * rb1;
+          sa_prev[i] = sa_cur;
+          acc[i][0] *= r0;
+          acc[i][0] = mfma_e4m3_16x16x128(wbuf[s][0], af, acc[i][0]);
+          acc[i][1] *= kSilu ? r1 : r0;
+          acc[i][1] = mfma_e4m3_16x16x128(wbuf[s][1], af, acc[i][1]);
+        };
+        frag_step(std::integral_constant<int, 0>{});
+        if (mf > 1) frag_step(std::integral_constant<int, 1>{});
+        if (mf > 2) frag_step(std::integral_constant<int, 2>{});
+        if (mf > 3) frag_step(std::integral_constant<int, 3>{});
+        __builtin_amdgcn_sched_barrier(0);
+        // loads P steps ahead: this item's step kt+P, or the next item's step s
+        const int ld_slot = cp_slot == 0 ? P : cp_slot - 1;
+        Load LL;
+        LL.wsrd = last_group ? Ln.wsrd : L.wsrd;
+        LL.ssrd = last_group ? Ln.ssrd : L.ssrd;
+        LL.a_voff = last_group ? Ln.a_voff : L.a_voff;
+        LL.as_voff = last_group ? Ln.as_voff : L.as_voff;
+        issue(LL, last_group ? s : kt + P, ld_slot, wbuf[s]);
+        cp_slot = cp_slot == P ? 0 : cp_slot + 1;
+      }
+    }
+
+    // ---- epilogue (the next item's first P steps are in flight) ----------
+    auto fac = [&](int i, int h) -> float { return sa_prev[i] * (h ? sb_prev1 : sb_prev0); };
+    if constexpr (!kSilu) {
+#pragma unroll
+      for (int i = 0; i < MF; ++i) {
+        const int r = 16 * i + l16;
+        if (i < mf && r < C.valid) {
+          const float f = fac(i, 0);
+          uint16_t* yrow = static_cast<uint16_t*>(p.c) + static_cast<int64_t>(C.row0 + r) * p.n_out +
+                           C.nt * kBN + 32 * wave + 4 * lg;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            uint2 v;
+            v.x = pack_bf16x2(acc[i][j][0] * f, acc[i][j][1] * f);
+            v.y = pack_bf16x2(acc[i][j][2] * f, acc[i][j][3] * f);
+            *reinterpret_cast<uint2*>(yrow + 16 * j) = v;
+          }
+        }
+      }
+    } else {
+      // h = bf16(SiLU(gate) * up) staged in LDS, then the row's 128 columns
+      // (one 1x128 group) requantised to e4m3 with their scale
+#pragma unroll
+      for (int i = 0; i < MF; ++i) {
+        if (i >= mf) break;
+        const float fg = fac(i, 0), fu = fac(i, 1);
+        float hv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) hv[q] = silu(acc[i][0][q] * fg) * (acc[i][1][q] * fu);
+        uint2 v;
+        v.x = pack_bf16x2(hv[0], hv[1]);
+        v.y = pack_bf16x2(hv[2], hv[3]);
+        lds_write_b64(lds_addr(ct + (16 * i + l16) * kNarrowCtLd + 16 * wave + 4 * lg), v);
+      }
+      lds_barrier();
+      if (tid < 2 * kNarrowRows) {
+        const int r = tid >> 1, half = tid & 1;
+        uint4 hrow[8];
+        lds_read_128B(lds_addr(ct + r * kNarrowCtLd + half * 64), hrow);
+        float m = 0.0f;
+        if (r < C.valid) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const uint4 v = hrow[u];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(w[q] & 0xffffu)), fabsf(bf16_bits_to_f32(w[q] >> 16))));
+          }
+        }
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        if (r < C.valid) {
+          const float sc = scale_from_amax(m);
+          const float inv = 1.0f / sc;
+          uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(C.row0 + r) * p.n_out +
+                         C.nt * 128 + half * 64;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            uint32_t qw[4];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+              const uint4 v = hrow[2 * u + h2];
+              const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+              for (int q = 0; q < 2; ++q) {
+                const uint32_t lo = w[2 * q], hi = w[2 * q + 1];
+                qw[h2 * 2 + q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(lo & 0xffffu), sc, inv),
+                                             quot_e4m3(bf16_bits_to_f32(lo >> 16), sc, inv),
+                                             quot_e4m3(bf16_bits_to_f32(hi & 0xffffu), sc, inv),
+                                             quot_e4m3(bf16_bits_to_f32(hi >> 16), sc, inv));
+              }
+            }
+            *reinterpret_cast<uint4*>(dst + u * 16) = uint4{qw[0], qw[1], qw[2], qw[3]};
+          }
+          if (half == 0) p.c_scale[static_cast<int64_t>(C.nt) * p.rows + C.row0 + r] = sc;
+        }
+      }
+      // the staging tile is next written after at least P more barriers
+    }
+    if (!have_next) break;
+    it_cur += grid;
+    L = Ln;
+    C = Cn;
+  }
+  // the re-loads issued after the last item land before the workgroup ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+}  // namespace hkmoe

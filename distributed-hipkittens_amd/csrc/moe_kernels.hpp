@@ -19,6 +19,7 @@ constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kScanThreads = 1024;
 constexpr int kTileCounters = 16;  // HKMOE_TILE_COUNTERS
+constexpr int kNarrowCounters = 2;  // narrow kernel item counters (GEMM 1, GEMM 2)
 
 __device__ __forceinline__ bool route_better(float av, int ai, float bv, int bi) {
   if (bi < 0) return ai >= 0;
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
     const int32_t* __restrict__ block_counts, int nblk, int num_experts, int e_stride, int parts,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ block_base,
     int32_t* __restrict__ mtile_offsets, int32_t* __restrict__ mtile_list, int tile_m,
-    float* amax_reset, int32_t* tile_counters) {
+    float* amax_reset, int32_t* tile_counters, int narrow_max, int32_t* narrow_info) {
   __shared__ int part_sum[kScanThreads];
   __shared__ int wave_tot[kScanThreads / 64];
   const int tid = threadIdx.x;
@@ -188,7 +189,9 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
   if (mtile_list != nullptr) {
     // M-tile list [(expert, first row)]: first the experts with at least one
     // full tile, each with all its tiles (full ones, then its partial one),
-    // in expert order; then the single partial tiles of the smaller experts.
+    // in expert order; then the single partial tiles of the smaller experts;
+    // last, with narrow_max > 0, the experts of 1..narrow_max rows, which the
+    // narrow kernel takes (their count goes to narrow_info[0]).
     // Tiles of nearly equal cost sit together in the grouped GEMMs' schedule,
     // so the workgroups that share a tile block stay in step and reuse its
     // operands in L2, and a large expert's partial tile runs while its
@@ -196,11 +199,17 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
     const int q_full = cnt / tile_m;
     const int q_part = (cnt % tile_m) ? 1 : 0;
     const int q_head = q_full > 0 ? q_full + q_part : 0;
-    const int q_tail = q_full > 0 ? 0 : q_part;
+    const int q_narrow = (q_full == 0 && cnt > 0 && cnt <= narrow_max) ? 1 : 0;
+    const int q_tail = (q_full > 0 || q_narrow) ? 0 : q_part;
     const int head_base = block_exclusive_scan(q_head, wave_tot);
     const int tail_base = block_exclusive_scan(q_tail, wave_tot);
-    __shared__ int n_head;
-    if (part == 0 && e == num_experts - 1) n_head = head_base + q_head;
+    const int narrow_base = block_exclusive_scan(q_narrow, wave_tot);
+    __shared__ int n_head, n_tail;
+    if (part == 0 && e == num_experts - 1) {
+      n_head = head_base + q_head;
+      n_tail = tail_base + q_tail;
+      if (narrow_info != nullptr) narrow_info[0] = narrow_base + q_narrow;
+    }
     __syncthreads();
     if (part == 0 && e < num_experts) {
       for (int s = 0; s < q_head; ++s) {
@@ -211,8 +220,13 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
         mtile_list[2 * (n_head + tail_base)] = e;
         mtile_list[2 * (n_head + tail_base) + 1] = off;
       }
+      if (q_narrow) {
+        mtile_list[2 * (n_head + n_tail + narrow_base)] = e;
+        mtile_list[2 * (n_head + n_tail + narrow_base) + 1] = off;
+      }
     }
   }
+  if (narrow_info != nullptr && tid >= 1 && tid < 1 + kNarrowCounters) narrow_info[tid] = 0;
   if (tid == 0 && amax_reset != nullptr) *amax_reset = 0.0f;
   if (tile_counters != nullptr && tid < kTileCounters) tile_counters[tid] = 0;
 }

@@ -653,6 +653,14 @@ PYBIND11_MODULE(tk_kernel, m) {
   m.def("dispatch_gemm_mx", &dispatch_gemm_mx, "C = A . B^T with 1x32 e8m0 scales (packed words)",
         py::arg("A"), py::arg("scale_a"), py::arg("B"), py::arg("scale_b"), py::arg("C"));
   m.def("moe_workspace_size", &moe_workspace_size);
+  m.def("set_narrow", [](int cus, int max_rows, int wide_share) { check(hkmoe_set_narrow(cus, max_rows, wide_share)); },
+        "narrow path of dispatch_moe: workgroups (0 = off), largest expert it takes, wide-GEMM CU share",
+        py::arg("cus"), py::arg("max_rows") = 64, py::arg("wide_share") = 0);
+  m.def("get_narrow", []() {
+    int32_t c = 0, r = 0, w = 0;
+    check(hkmoe_get_narrow(&c, &r, &w));
+    return py::make_tuple(c, r, w);
+  });
   m.def("route_blocks", [](int64_t t) { return hkmoe_route_blocks(t); });
   m.def("mtile_list_ints", &mtile_list_ints, "ints of an M-tile list for `rows` expert rows over E experts");
   m.def("version", []() { return hkmoe_version(); });

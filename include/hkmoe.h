@@ -175,8 +175,11 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
 /*
  * Load-time weight packing for the grouped GEMMs: w [E, N, K] e4m3 row-major
  * -> packed (E*N*K bytes, another buffer).  Every 256-row N tile x 128-byte
- * K step becomes one contiguous 32 KiB block in the GEMM's LDS stage order,
- * so a tile's weights stream sequentially.  gate_up = I for the fused gate/up
+ * K step becomes one contiguous 32 KiB block holding its sixteen 16-row MFMA
+ * fragments in operand-register order (each fragment as two 1 KiB register
+ * halves: byte f*2048 + h*1024 + l*16 + b = row 16f + l%16, K byte
+ * (2*(l/16) + h)*16 + b), so a tile's weights stream sequentially and every
+ * 64-lane load of a register half reads 1 KiB of whole cache lines.  gate_up = I for the fused gate/up
  * weights of GEMM 1 (N = 2I: rows [gate | up]), 0 otherwise.
  * Requires N % 256 == 0, K % 128 == 0 (gate_up: N == 2*gate_up).
  * No reference counterpart (the reference's GEMMs read [N, K] rows directly);
@@ -204,6 +207,24 @@ int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, i
  */
 size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k,
                                 int32_t hidden, int32_t inter, int scale_mode);
+/*
+ * Narrow path of hkmoe_moe_forward (block scales only): the experts with
+ * 1..max_rows rows (max_rows <= 64) go to a weight-streaming grouped GEMM
+ * (both GEMMs) that runs on `cus` workgroups on a library-owned auxiliary
+ * stream, beside the 256x256 kernels of the larger experts on the caller's
+ * stream; the caller's stream waits for it before the combine.  Results are
+ * bit-identical with the narrow path on or off.  cus == 0 turns it off;
+ * wide_share != 0 launches the first wide GEMM on (CUs - cus) workgroups.
+ * It also stays off when H/128 or I/128 is odd, and for a first call made
+ * while the caller's stream is being captured into a graph (the auxiliary
+ * stream is created on the first call that is not captured).  Defaults come
+ * from HKMOE_NARROW_CUS, HKMOE_NARROW_MAX and HKMOE_NARROW_SHARE in the
+ * environment, else 48, 64 and 1.  Concurrent hkmoe_moe_forward calls on one
+ * device enqueue their fork/join one at a time (a mutex).
+ * No reference counterpart: the reference has no grouped GEMM.
+ */
+int hkmoe_set_narrow(int32_t cus, int32_t max_rows, int32_t wide_share);
+int hkmoe_get_narrow(int32_t* cus, int32_t* max_rows, int32_t* wide_share);
 int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
                       const float* w13_scale, const void* w2, const float* w2_scale,
                       int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
