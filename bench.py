@@ -193,9 +193,12 @@ def kernel_breakdown(inp, layer, iters=10):
         return kernel_breakdown_mx(inp, layer, iters)
     pk = layer.packed
     w13, w2 = layer.w13_q, layer.w2_q
+    block = inp["x_scale"].dim() == 2
+    narrow = narrow_setting(inp)
+    if narrow is not None:
+        return kernel_breakdown_narrow(inp, layer, narrow, iters)
     r = hkmoe.moe_forward_steps(inp["x_q"], inp["x_scale"], inp["logits"], w13,
                                 inp["w13_scale"], w2, inp["w2_scale"], inp["top_k"], packed=pk)
-    block = inp["x_scale"].dim() == 2
     T = inp["x_q"].shape[0]
     k = inp["top_k"]
     calls = [
@@ -224,6 +227,88 @@ def kernel_breakdown(inp, layer, iters=10):
             ev[name].append((s, e))
     torch.cuda.synchronize()
     ms = {name: sum(s.elapsed_time(e) for s, e in lst) / len(lst) for name, lst in ev.items()}
+    return ms, r
+
+
+def narrow_setting(inp):
+    """(cus, max_rows, share) of the layer's narrow path, or None when the
+    layer runs without it (per-tensor scales, odd K-step counts, turned off)."""
+    import tk_kernel
+    cus, max_rows, share = tk_kernel.get_narrow()
+    hidden = inp["x_q"].shape[1]
+    inter = inp["w2_q"].shape[2]
+    if inp["x_scale"].dim() != 2 or cus <= 0 or max_rows <= 0 or (hidden // 128) % 2 or (inter // 128) % 2:
+        return None
+    return cus, max_rows, share
+
+
+def kernel_breakdown_narrow(inp, layer, narrow, iters=10):
+    """Per-kernel average ms of the split layer: the 256x256 GEMMs on the current
+    stream and the narrow GEMMs on a side stream, enqueued as hkmoe_moe_forward
+    does (events on the stream each kernel runs on), plus GEMM 1's span over
+    both of its kernels."""
+    import torch
+    import tk_kernel
+    import hkmoe
+    cus, max_rows, share = narrow
+    pk = layer.packed
+    w13, w2 = layer.w13_q, layer.w2_q
+    k = inp["top_k"]
+    T = inp["x_q"].shape[0]
+    r = hkmoe.moe_forward_steps(inp["x_q"], inp["x_scale"], inp["logits"], w13, inp["w13_scale"], w2,
+                                inp["w2_scale"], k, packed=pk, narrow=narrow)
+    dev = inp["x_q"].device
+    main = torch.cuda.current_stream(dev)
+    side = r["side"]
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    split = dict(packed=pk, mtile_list=r["mtile_list"], narrow_info=r["narrow_info"])
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    route = [
+        ("route_topk", lambda: tk_kernel.dispatch_route_topk(inp["logits"], r["topk_idx"], r["topk_w"], r["block_counts"])),
+        ("expert_offsets", lambda: tk_kernel.dispatch_expert_offsets(r["block_counts"], T, r["counts"], r["offsets"], r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"], r["mtile_list"], narrow_max=max_rows, narrow_info=r["narrow_info"])),
+        ("scatter", lambda: tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"], r["inv_perm"], None, None, None, None)),
+    ]
+    acc = {n: [] for n in ("route_topk", "expert_offsets", "scatter", "grouped_gemm1", "narrow_gemm1",
+                           "gemm1_span", "grouped_gemm2", "narrow_gemm2", "combine")}
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        marks = {}
+        for name, fn in route:
+            a, b = ev(), ev()
+            a.record(main)
+            fn()
+            b.record(main)
+            marks[name] = (a, b)
+        e0, e1, e2, s0, s1, s2 = ev(), ev(), ev(), ev(), ev(), ev()
+        e0.record(main)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            s0.record(side)
+            tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], None, part=1, grid=cus, **split)
+            s1.record(side)
+            tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2, inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], None, part=1, grid=cus, **split)
+            s2.record(side)
+        tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8], part=0, grid=max(1, n_cu - cus) if share else 0, **split)
+        e1.record(main)
+        tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2, inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], r["tile_ctr"][8:], part=0, grid=0, **split)
+        e2.record(main)
+        main.wait_stream(side)
+        c0, c1 = ev(), ev()
+        c0.record(main)
+        tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])
+        c1.record(main)
+        marks.update(grouped_gemm1=(e0, e1), narrow_gemm1=(s0, s1), grouped_gemm2=(e1, e2),
+                     narrow_gemm2=(s1, s2), combine=(c0, c1), gemm1_span=(e0, (e1, s1)))
+        acc_marks = marks
+        for n in acc:
+            acc[n].append(acc_marks[n])
+    torch.cuda.synchronize()
+    ms = {}
+    for n, lst in acc.items():
+        if n == "gemm1_span":
+            ms[n] = sum(max(a.elapsed_time(b1), a.elapsed_time(b2)) for a, (b1, b2) in lst) / len(lst)
+        else:
+            ms[n] = sum(a.elapsed_time(b) for a, b in lst) / len(lst)
     return ms, r
 
 
@@ -619,7 +704,16 @@ def main():
         del src, dst
     ms, r = kernel_breakdown(inp, layer)
     rows = cfg["T"] * cfg["k"]
-    g1_flops = 2.0 * rows * 2 * cfg["I"] * cfg["H"]
+    counts = r["counts"].cpu()
+    narrow = r.get("narrow_info") is not None
+    narrow_rows = 0
+    if narrow:
+        _, max_rows, _ = narrow_setting(inp)
+        small = (counts > 0) & (counts <= max_rows)
+        narrow_rows = int(counts[small].sum())
+        n_narrow = int(small.sum())
+    # the dominant kernel is the 256x256 GEMM 1 over the rows it processes
+    g1_flops = 2.0 * (rows - narrow_rows) * 2 * cfg["I"] * cfg["H"]
     g1_tflops = g1_flops / (ms["grouped_gemm1"] * 1e-3) / 1e12
     traffic = None
     if os.path.exists(args.traffic):
@@ -628,7 +722,6 @@ def main():
                 traffic = json.load(f).get(f"{args.config}:grouped_gemm1")
         except Exception:
             traffic = None
-    counts = r["counts"].cpu()
     res = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
@@ -642,13 +735,30 @@ def main():
                    "weights": args.weights, "launch": "hip_graph" if args.graph else "eager",
                    "active_experts": int((counts > 0).sum()), "max_rows": int(counts.max())},
         "pct_fp8_peak": round(100.0 * value / PEAK_FP8_TFLOPS, 2),
-        "roofline": {"bound": "mfma", "kernel": "grouped_gemm1 (gate/up + SiLU*up)",
+        "roofline": {"bound": "mfma",
+                     "kernel": ("grouped_gemm1 256x256 (gate/up + SiLU*up), experts above the narrow "
+                                "threshold" if narrow else "grouped_gemm1 (gate/up + SiLU*up)"),
                      "achieved": round(g1_tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(g1_tflops / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
                      "avg_ms": round(ms["grouped_gemm1"], 4), "flops_per_launch": g1_flops},
         "kernels_ms": {k: round(v, 4) for k, v in ms.items()},
         "gemm_only_tflops": round(flops / ((ms["grouped_gemm1"] + ms["grouped_gemm2"]) * 1e-3) / 1e12, 2),
     }
+    if narrow:
+        # narrow kernels stream the small experts' weights: HBM-bound
+        cus, max_rows, share = narrow_setting(inp)
+        nb1 = n_narrow * 2 * cfg["I"] * cfg["H"]
+        nb2 = n_narrow * cfg["H"] * cfg["I"]
+        res["narrow"] = {
+            "experts": n_narrow, "rows": narrow_rows, "max_rows": max_rows, "cus": cus, "wide_share": share,
+            "gemm1": {"ms": round(ms["narrow_gemm1"], 4), "weight_bytes": nb1,
+                      "GB_s": round(nb1 / ms["narrow_gemm1"] / 1e6, 1)},
+            "gemm2": {"ms": round(ms["narrow_gemm2"], 4), "weight_bytes": nb2,
+                      "GB_s": round(nb2 / ms["narrow_gemm2"] / 1e6, 1)},
+            "gemm1_span_ms": round(ms["gemm1_span"], 4),
+            "gemm1_span_tflops": round(2.0 * rows * 2 * cfg["I"] * cfg["H"] / (ms["gemm1_span"] * 1e-3) / 1e12, 2),
+        }
+        res.pop("gemm_only_tflops")
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(inp, cfg, args.cpu_seconds)
     print(json.dumps(res), flush=True)

@@ -304,6 +304,24 @@ int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_
                                static_cast<hipStream_t>(stream));
 }
 
+int hkmoe_expert_offsets_narrow(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
+                                int32_t* counts, int32_t* offsets, int32_t* block_base,
+                                int32_t* mtile_offsets, int32_t* mtile_list, float* amax_reset,
+                                int32_t* tile_counters, int32_t narrow_max, int32_t* narrow_info,
+                                hkmoe_stream_t stream) {
+  HK_REQUIRE(counts && offsets && block_base && mtile_offsets && mtile_list && narrow_info,
+             "expert_offsets_narrow: null pointer");
+  HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "expert_offsets_narrow: E=%d outside [1, %d]",
+             num_experts, kMaxExperts);
+  HK_REQUIRE(num_tokens >= 0, "expert_offsets_narrow: bad T");
+  HK_REQUIRE(num_tokens == 0 || block_counts, "expert_offsets_narrow: null block_counts");
+  HK_REQUIRE(narrow_max >= 0 && narrow_max <= kNarrowRows, "expert_offsets_narrow: narrow_max=%d outside [0, %d]",
+             narrow_max, kNarrowRows);
+  return launch_expert_offsets(block_counts, num_tokens, num_experts, counts, offsets, block_base,
+                               mtile_offsets, mtile_list, amax_reset, tile_counters, narrow_max, narrow_info,
+                               static_cast<hipStream_t>(stream));
+}
+
 int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_experts, int32_t top_k,
                   const int32_t* offsets, const int32_t* block_base, int32_t* perm, int32_t* inv_perm,
                   const void* x_q, const float* x_scale, int64_t hidden, int scale_mode, void* xp,
@@ -500,6 +518,42 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
                         int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream) {
   return grouped_gemm2_impl(hq, hs, w2, w2_scale, offsets, mtile_offsets, mtile_list, rows, num_experts,
                             hidden, inter, scale_mode, w_layout, y, tile_counters, stream, nullptr, 0, 0);
+}
+
+int hkmoe_grouped_gemm1_part(const void* x, const float* x_scale, const int32_t* gather,
+                             int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
+                             const int32_t* offsets, const int32_t* mtile_offsets,
+                             const int32_t* mtile_list, int64_t rows, int32_t num_experts, int32_t hidden,
+                             int32_t inter, int w_layout, void* hq, float* hs, int32_t* tile_counters,
+                             const int32_t* narrow_info, int32_t part, int32_t grid, hkmoe_stream_t stream) {
+  HK_REQUIRE(narrow_info && mtile_list, "grouped_gemm1_part: needs narrow_info and mtile_list");
+  HK_REQUIRE(part == 0 || part == 1, "grouped_gemm1_part: part=%d must be 0 (wide) or 1 (narrow)", part);
+  HK_REQUIRE(grid >= 0 && grid <= 65536, "grouped_gemm1_part: bad grid %d", grid);
+  HK_REQUIRE(part == 0 || narrow_depth(hidden / kBK) > 0,
+             "grouped_gemm1_part: the narrow kernel needs an even number of 128-wide K steps (H=%d)", hidden);
+  if (part == 1) {
+    return grouped_gemm1_impl(x, x_scale, gather, gather_div, x_rows, w13, w13_scale, offsets, mtile_offsets,
+                              mtile_list, rows, num_experts, hidden, inter, HKMOE_SCALE_BLOCK, w_layout,
+                              HKMOE_E4M3, hq, hs, nullptr, stream, narrow_info, 0, grid > 0 ? grid : device_cus());
+  }
+  return grouped_gemm1_impl(x, x_scale, gather, gather_div, x_rows, w13, w13_scale, offsets, mtile_offsets,
+                            mtile_list, rows, num_experts, hidden, inter, HKMOE_SCALE_BLOCK, w_layout, HKMOE_E4M3,
+                            hq, hs, tile_counters, stream, narrow_info, grid, 0);
+}
+
+int hkmoe_grouped_gemm2_part(const void* hq, const float* hs, const void* w2, const float* w2_scale,
+                             const int32_t* offsets, const int32_t* mtile_offsets, const int32_t* mtile_list,
+                             int64_t rows, int32_t num_experts, int32_t hidden, int32_t inter, int w_layout,
+                             void* y, int32_t* tile_counters, const int32_t* narrow_info, int32_t part,
+                             int32_t grid, hkmoe_stream_t stream) {
+  HK_REQUIRE(narrow_info && mtile_list, "grouped_gemm2_part: needs narrow_info and mtile_list");
+  HK_REQUIRE(part == 0 || part == 1, "grouped_gemm2_part: part=%d must be 0 (wide) or 1 (narrow)", part);
+  HK_REQUIRE(grid >= 0 && grid <= 65536, "grouped_gemm2_part: bad grid %d", grid);
+  HK_REQUIRE(part == 0 || narrow_depth(inter / kBK) > 0,
+             "grouped_gemm2_part: the narrow kernel needs an even number of 128-wide K steps (I=%d)", inter);
+  return grouped_gemm2_impl(hq, hs, w2, w2_scale, offsets, mtile_offsets, mtile_list, rows, num_experts, hidden,
+                            inter, HKMOE_SCALE_BLOCK, w_layout, y, part == 1 ? nullptr : tile_counters, stream,
+                            narrow_info, part == 0 ? grid : 0, part == 1 ? (grid > 0 ? grid : device_cus()) : 0);
 }
 
 int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k, int32_t gate_up,

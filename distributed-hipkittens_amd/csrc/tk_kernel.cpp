@@ -146,7 +146,11 @@ int64_t mtile_list_ints(int64_t rows, int64_t e) { return 2 * ((rows + 255) / 25
 
 void dispatch_expert_offsets(py::object bc, int64_t num_tokens, py::object counts, py::object offsets,
                              py::object block_base, py::object mtile_offsets, py::object amax,
-                             py::object tile_counters, py::object mtile_list) {
+                             py::object tile_counters, py::object mtile_list, int32_t narrow_max,
+                             py::object narrow_info) {
+  auto ni = as_tensor_opt(narrow_info, "narrow_info");
+  want_dtype(ni, "narrow_info", kI32);
+  if (ni.ptr && ni.numel() < 3) throw std::runtime_error("narrow_info must hold 3 ints");
   auto b = as_tensor(bc, "block_counts"), c = as_tensor(counts, "counts"),
        o = as_tensor(offsets, "offsets"), bb = as_tensor(block_base, "block_base"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), am = as_tensor_opt(amax, "amax"),
@@ -162,6 +166,15 @@ void dispatch_expert_offsets(py::object bc, int64_t num_tokens, py::object count
     throw std::runtime_error("block_counts/block_base too small");
   if (ml.ptr && ml.numel() < mtile_list_ints(num_tokens * std::min<int64_t>(e, 32), e))
     throw std::runtime_error("mtile_list must hold 2 * (ceil(T * min(E, 32) / 256) + E) ints");
+  if (ni.ptr) {
+    check(hkmoe_expert_offsets_narrow(static_cast<const int32_t*>(b.ptr), num_tokens, static_cast<int32_t>(e),
+                                      static_cast<int32_t*>(c.ptr), static_cast<int32_t*>(o.ptr),
+                                      static_cast<int32_t*>(bb.ptr), static_cast<int32_t*>(mo.ptr),
+                                      static_cast<int32_t*>(ml.ptr), static_cast<float*>(am.ptr),
+                                      static_cast<int32_t*>(tc.ptr), narrow_max, static_cast<int32_t*>(ni.ptr),
+                                      current_stream()));
+    return;
+  }
   check(hkmoe_expert_offsets(static_cast<const int32_t*>(b.ptr), num_tokens, static_cast<int32_t>(e),
                              static_cast<int32_t*>(c.ptr), static_cast<int32_t*>(o.ptr),
                              static_cast<int32_t*>(bb.ptr), static_cast<int32_t*>(mo.ptr),
@@ -208,7 +221,9 @@ void dispatch_scatter(py::object idx, py::object offsets, py::object block_base,
 void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gather, int32_t gather_div,
                             py::object w13, py::object w13s, py::object offsets, py::object mtile_offsets,
                             py::object h, py::object h_aux, py::object tile_counters, bool packed,
-                            py::object mtile_list) {
+                            py::object mtile_list, py::object narrow_info, int32_t part, int32_t grid) {
+  auto ni = as_tensor_opt(narrow_info, "narrow_info");
+  want_dtype(ni, "narrow_info", kI32);
   auto x = as_tensor(x_q, "x"), xs = as_tensor(x_scale, "x_scale"), gth = as_tensor_opt(gather, "gather"),
        w = as_tensor(w13, "w13"), ws = as_tensor(w13s, "w13_scale"), o = as_tensor(offsets, "offsets"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), hh = as_tensor(h, "h"),
@@ -244,6 +259,19 @@ void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gathe
     throw std::runtime_error("block scales: x_scale [x_rows, H/128], w13_scale [E, 2I/128, H/128]");
   if (fmt == HKMOE_E4M3 && (!aux.ptr || aux.numel() != rows * (inter / 128)))
     throw std::runtime_error("e4m3 output needs h_aux [I/128, rows] group scales");
+  if (ni.ptr) {
+    if (mode != HKMOE_SCALE_BLOCK || fmt != HKMOE_E4M3 || !ml.ptr)
+      throw std::runtime_error("narrow split: needs block scales, e4m3 h and the M-tile list");
+    check(hkmoe_grouped_gemm1_part(x.ptr, static_cast<const float*>(xs.ptr), static_cast<const int32_t*>(gth.ptr),
+                                   gather_div, x_rows, w.ptr, static_cast<const float*>(ws.ptr),
+                                   static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr),
+                                   static_cast<const int32_t*>(ml.ptr), rows, static_cast<int32_t>(e),
+                                   static_cast<int32_t>(hidden), static_cast<int32_t>(inter),
+                                   packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, hh.ptr, static_cast<float*>(aux.ptr),
+                                   static_cast<int32_t*>(tc.ptr), static_cast<const int32_t*>(ni.ptr), part, grid,
+                                   current_stream()));
+    return;
+  }
   check(hkmoe_grouped_gemm1(x.ptr, static_cast<const float*>(xs.ptr), static_cast<const int32_t*>(gth.ptr),
                             gather_div, x_rows, w.ptr, static_cast<const float*>(ws.ptr),
                             static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr),
@@ -274,7 +302,10 @@ void dispatch_requant(py::object h, py::object amax, py::object hq, py::object h
 
 void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::object w2s,
                             py::object offsets, py::object mtile_offsets, py::object y,
-                            py::object tile_counters, bool packed, py::object mtile_list) {
+                            py::object tile_counters, bool packed, py::object mtile_list,
+                            py::object narrow_info, int32_t part, int32_t grid) {
+  auto ni = as_tensor_opt(narrow_info, "narrow_info");
+  want_dtype(ni, "narrow_info", kI32);
   auto q = as_tensor(hq, "hq"), s = as_tensor(hs, "hs"), w = as_tensor(w2, "w2"),
        ws = as_tensor(w2s, "w2_scale"), o = as_tensor(offsets, "offsets"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), yy = as_tensor(y, "y"),
@@ -299,6 +330,18 @@ void dispatch_grouped_gemm2(py::object hq, py::object hs, py::object w2, py::obj
   if (mode == HKMOE_SCALE_BLOCK &&
       (s.numel() != rows * (inter / 128) || ws.numel() != e * (hidden / 128) * (inter / 128)))
     throw std::runtime_error("block scales: hs [I/128, rows], w2_scale [E, H/128, I/128]");
+  if (ni.ptr) {
+    if (mode != HKMOE_SCALE_BLOCK || !ml.ptr)
+      throw std::runtime_error("narrow split: needs block scales and the M-tile list");
+    check(hkmoe_grouped_gemm2_part(q.ptr, static_cast<const float*>(s.ptr), w.ptr,
+                                   static_cast<const float*>(ws.ptr), static_cast<const int32_t*>(o.ptr),
+                                   static_cast<const int32_t*>(mo.ptr), static_cast<const int32_t*>(ml.ptr), rows,
+                                   static_cast<int32_t>(e), static_cast<int32_t>(hidden),
+                                   static_cast<int32_t>(inter), packed ? HKMOE_W_PACKED : HKMOE_W_ROWS, yy.ptr,
+                                   static_cast<int32_t*>(tc.ptr), static_cast<const int32_t*>(ni.ptr), part, grid,
+                                   current_stream()));
+    return;
+  }
   check(hkmoe_grouped_gemm2(q.ptr, static_cast<const float*>(s.ptr), w.ptr,
                             static_cast<const float*>(ws.ptr), static_cast<const int32_t*>(o.ptr),
                             static_cast<const int32_t*>(mo.ptr), static_cast<const int32_t*>(ml.ptr), rows,
@@ -615,16 +658,18 @@ PYBIND11_MODULE(tk_kernel, m) {
   m.def("dispatch_expert_offsets", &dispatch_expert_offsets, py::arg("block_counts"), py::arg("num_tokens"),
         py::arg("counts"), py::arg("offsets"), py::arg("block_base"), py::arg("mtile_offsets"),
         py::arg("amax") = py::none(), py::arg("tile_counters") = py::none(),
-        py::arg("mtile_list") = py::none());
+        py::arg("mtile_list") = py::none(), py::arg("narrow_max") = 0, py::arg("narrow_info") = py::none());
   m.def("dispatch_scatter", &dispatch_scatter);
   m.def("dispatch_grouped_gemm1", &dispatch_grouped_gemm1, py::arg("x_q"), py::arg("x_scale"), py::arg("gather"),
         py::arg("gather_div"), py::arg("w13"), py::arg("w13_scale"), py::arg("offsets"),
         py::arg("mtile_offsets"), py::arg("h"), py::arg("h_aux") = py::none(),
-        py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none());
+        py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none(),
+        py::arg("narrow_info") = py::none(), py::arg("part") = 0, py::arg("grid") = 0);
   m.def("dispatch_requant", &dispatch_requant);
   m.def("dispatch_grouped_gemm2", &dispatch_grouped_gemm2, py::arg("hq"), py::arg("hs"), py::arg("w2"),
         py::arg("w2_scale"), py::arg("offsets"), py::arg("mtile_offsets"), py::arg("y"),
-        py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none());
+        py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none(),
+        py::arg("narrow_info") = py::none(), py::arg("part") = 0, py::arg("grid") = 0);
   m.def("dispatch_combine", &dispatch_combine);
   m.def("dispatch_moe", &dispatch_moe, py::arg("x_q"), py::arg("x_scale"), py::arg("logits"), py::arg("w13"),
         py::arg("w13_scale"), py::arg("w2"), py::arg("w2_scale"), py::arg("top_k"), py::arg("out"),

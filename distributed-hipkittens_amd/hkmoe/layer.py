@@ -127,10 +127,15 @@ def moe_forward(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k,
 
 
 def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k,
-                      keep_h=False, packed=False):
+                      keep_h=False, packed=False, narrow=None):
     """The layer one kernel at a time (the same kernels hkmoe_moe_forward
     enqueues); returns a dict of every intermediate.  With ``keep_h`` the block
-    path also runs GEMM 1 once more with a bf16 output (``h``) for inspection."""
+    path also runs GEMM 1 once more with a bf16 output (``h``) for inspection.
+    ``narrow = (cus, max_rows, share)`` (block scales) splits both GEMMs like
+    hkmoe_moe_forward's narrow path: the experts of <= max_rows rows run in the
+    narrow kernel on ``cus`` workgroups on a side stream (``r["side"]``), the
+    others in the 256x256 kernel on the current stream (on CUs - cus
+    workgroups for GEMM 1 with ``share``)."""
     _check_dev(x_q, logits, w13_q, w2_q)
     dev = x_q.device
     t, hidden = x_q.shape
@@ -156,6 +161,11 @@ def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, to
     )
     if not block or keep_h:
         r["h"] = torch.empty((rows, inter), dtype=torch.bfloat16, device=dev)
+    if narrow is not None:
+        if not block:
+            raise RuntimeError("moe_forward_steps: the narrow split needs block scales")
+        return _steps_narrow(r, x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k, packed,
+                             narrow)
     tk_kernel.dispatch_route_topk(logits, r["topk_idx"], r["topk_w"], r["block_counts"])
     tk_kernel.dispatch_expert_offsets(r["block_counts"], t, r["counts"], r["offsets"],
                                       r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"],
@@ -179,6 +189,38 @@ def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, to
                                      r["mtile_offsets"], r["y"], r["tile_ctr"][8:],
                                      packed=packed, mtile_list=r["mtile_list"])
     tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])
+    return r
+
+
+def _steps_narrow(r, x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k, packed, narrow):
+    cus, max_rows, share = narrow
+    t = x_q.shape[0]
+    dev = x_q.device
+    r["narrow_info"] = torch.zeros(3, dtype=torch.int32, device=dev)
+    tk_kernel.dispatch_route_topk(logits, r["topk_idx"], r["topk_w"], r["block_counts"])
+    tk_kernel.dispatch_expert_offsets(r["block_counts"], t, r["counts"], r["offsets"],
+                                      r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"],
+                                      r["mtile_list"], narrow_max=max_rows, narrow_info=r["narrow_info"])
+    tk_kernel.dispatch_scatter(r["topk_idx"], r["offsets"], r["block_base"], r["perm"],
+                               r["inv_perm"], None, None, None, None)
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(main)
+    split = dict(packed=packed, mtile_list=r["mtile_list"], narrow_info=r["narrow_info"])
+    with torch.cuda.stream(side):
+        tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale, r["offsets"],
+                                         r["mtile_offsets"], r["hq"], r["hs"], None, part=1, grid=cus, **split)
+        tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2_q, w2_scale, r["offsets"], r["mtile_offsets"],
+                                         r["y"], None, part=1, grid=cus, **split)
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale, r["offsets"],
+                                     r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8], part=0,
+                                     grid=max(1, n_cu - cus) if share else 0, **split)
+    tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2_q, w2_scale, r["offsets"], r["mtile_offsets"],
+                                     r["y"], r["tile_ctr"][8:], part=0, grid=0, **split)
+    main.wait_stream(side)
+    tk_kernel.dispatch_combine(r["y"], r["topk_w"], r["inv_perm"], r["out"])
+    r["side"] = side
     return r
 
 

@@ -173,6 +173,39 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
                         int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream);
 
 /*
+ * The same layer split for the narrow path of hkmoe_moe_forward (block scales,
+ * e4m3 h), for callers that enqueue the parts themselves:
+ *   hkmoe_expert_offsets_narrow: hkmoe_expert_offsets that also moves the experts
+ *     of 1..narrow_max rows (narrow_max <= 64) to the end of the M-tile list,
+ *     writes their count to narrow_info[0] and zeroes narrow_info[1..2]
+ *     (narrow_info: 3 int32 of device memory).
+ *   hkmoe_grouped_gemm{1,2}_part: part 0 runs the 256x256 kernel on the list
+ *     without those experts (grid 0: one workgroup per CU, else `grid`); part 1
+ *     runs the narrow kernel on exactly those experts with `grid` workgroups
+ *     (0: one per CU) and takes no tile counters; its K steps per item (H/128,
+ *     I/128) must be even.  The two parts write disjoint rows and may run
+ *     concurrently on two streams; together they give the bits of
+ *     hkmoe_grouped_gemm{1,2}.
+ * No reference counterpart (the reference has no grouped GEMM).
+ */
+int hkmoe_expert_offsets_narrow(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
+                                int32_t* counts, int32_t* offsets, int32_t* block_base,
+                                int32_t* mtile_offsets, int32_t* mtile_list, float* amax_reset,
+                                int32_t* tile_counters, int32_t narrow_max, int32_t* narrow_info,
+                                hkmoe_stream_t stream);
+int hkmoe_grouped_gemm1_part(const void* x, const float* x_scale, const int32_t* gather,
+                             int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
+                             const int32_t* offsets, const int32_t* mtile_offsets,
+                             const int32_t* mtile_list, int64_t rows, int32_t num_experts, int32_t hidden,
+                             int32_t inter, int w_layout, void* hq, float* hs, int32_t* tile_counters,
+                             const int32_t* narrow_info, int32_t part, int32_t grid, hkmoe_stream_t stream);
+int hkmoe_grouped_gemm2_part(const void* hq, const float* hs, const void* w2, const float* w2_scale,
+                             const int32_t* offsets, const int32_t* mtile_offsets, const int32_t* mtile_list,
+                             int64_t rows, int32_t num_experts, int32_t hidden, int32_t inter, int w_layout,
+                             void* y, int32_t* tile_counters, const int32_t* narrow_info, int32_t part,
+                             int32_t grid, hkmoe_stream_t stream);
+
+/*
  * Load-time weight packing for the grouped GEMMs: w [E, N, K] e4m3 row-major
  * -> packed (E*N*K bytes, another buffer).  Every 256-row N tile x 128-byte
  * K step becomes one contiguous 32 KiB block holding its sixteen 16-row MFMA

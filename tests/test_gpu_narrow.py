@@ -84,6 +84,29 @@ def test_narrow_bit_exact(hk, narrow_restore, name, packed):
         assert torch.equal(y.view(torch.int16), off.view(torch.int16))
 
 
+@pytest.mark.parametrize("packed", [True, False])
+@pytest.mark.parametrize("name", ["p8_g2_g1", "p4_p2"])
+def test_split_steps_bit_exact(hk, name, packed):
+    """The stepwise split (hkmoe_expert_offsets_narrow + hkmoe_grouped_gemm{1,2}_part
+    on two streams) gives the 256x256-only intermediates bit for bit, and
+    narrow_info holds the count of experts of 1..max_rows rows."""
+    c = CASES[name]
+    g = _dev_inputs(hk, seed=33, **c)
+    w13, w2 = g["w13_q"], g["w2_q"]
+    if packed:
+        w13, w2 = hk.pack_weights(w13, gate_up=True), hk.pack_weights(w2)
+    args = (g["x_q"], g["x_scale"], g["logits"], w13, g["w13_scale"], w2, g["w2_scale"], g["top_k"])
+    ref = hk.moe_forward_steps(*args, packed=packed)
+    for narrow in ((48, 64, 1), (5, 32, 0)):
+        r = hk.moe_forward_steps(*args, packed=packed, narrow=narrow)
+        torch.cuda.synchronize()
+        counts = r["counts"].cpu()
+        want = int(((counts > 0) & (counts <= narrow[1])).sum())
+        assert int(r["narrow_info"][0]) == want and want > 0
+        for key in ("hq", "hs", "y", "out"):
+            assert torch.equal(r[key].view(torch.uint8), ref[key].view(torch.uint8)), (narrow, key)
+
+
 def test_narrow_oracle(hk, narrow_restore):
     """A small skewed layer with the narrow path on vs the numpy oracle (<= 1e-2)."""
     d = synth.make_moe(T=200, H=512, I=256, E=24, k=3, block=True, skew=True, seed=41)
