@@ -261,6 +261,7 @@ def kernel_breakdown_narrow(inp, layer, narrow, iters=10):
     main = torch.cuda.current_stream(dev)
     side = r["side"]
     n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    grid = hkmoe.layer.narrow_grid(T * k, w13.shape[0], cus, max_rows, n_cu)
     split = dict(packed=pk, mtile_list=r["mtile_list"], narrow_info=r["narrow_info"])
     ev = lambda: torch.cuda.Event(enable_timing=True)
     route = [
@@ -284,9 +285,9 @@ def kernel_breakdown_narrow(inp, layer, narrow, iters=10):
         side.wait_stream(main)
         with torch.cuda.stream(side):
             s0.record(side)
-            tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], None, part=1, grid=cus, **split)
+            tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], None, part=1, grid=grid, **split)
             s1.record(side)
-            tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2, inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], None, part=1, grid=cus, **split)
+            tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2, inp["w2_scale"], r["offsets"], r["mtile_offsets"], r["y"], None, part=1, grid=grid, **split)
             s2.record(side)
         tk_kernel.dispatch_grouped_gemm1(inp["x_q"], inp["x_scale"], r["perm"], k, w13, inp["w13_scale"], r["offsets"], r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8], part=0, grid=max(1, n_cu - cus) if share else 0, **split)
         e1.record(main)
@@ -758,6 +759,13 @@ def main():
             "gemm1_span_ms": round(ms["gemm1_span"], 4),
             "gemm1_span_tflops": round(2.0 * rows * 2 * cfg["I"] * cfg["H"] / (ms["gemm1_span"] * 1e-3) / 1e12, 2),
         }
+        if narrow_rows == rows:
+            # every expert is narrow (decode-like): the dominant kernel is the
+            # narrow GEMM 1, bound by streaming the experts' weights from HBM
+            res["roofline"] = {"bound": "hbm", "kernel": "narrow grouped_gemm1 (gate/up + SiLU*up)",
+                               "achieved": round(nb1 / ms["narrow_gemm1"] / 1e6, 1), "peak": PEAK_HBM_GBS,
+                               "unit": "GB/s", "frac": round(nb1 / ms["narrow_gemm1"] / 1e6 / PEAK_HBM_GBS, 4),
+                               "traffic": None, "avg_ms": round(ms["narrow_gemm1"], 4), "bytes_per_launch": nb1}
         res.pop("gemm_only_tflops")
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(inp, cfg, args.cpu_seconds)

@@ -133,12 +133,12 @@ int launch_narrow(GemmParams p, hipStream_t stream, int grid) {
 }
 
 // Narrow path settings, read once from the environment:
-//   HKMOE_NARROW_CUS   workgroups (CUs) of the narrow kernels, 0 = off (default 48)
+//   HKMOE_NARROW_CUS   workgroups (CUs) of the narrow kernels, 0 = off (default 64)
 //   HKMOE_NARROW_MAX   largest expert (rows) the narrow kernel takes, <= 64 (default 64)
 //   HKMOE_NARROW_SHARE 1: the first wide GEMM leaves those CUs to the narrow
-//                      kernel (grid = CUs - HKMOE_NARROW_CUS); 0: full grid (default 1).
-//                      A full-grid wide GEMM takes every CU first, and the narrow
-//                      kernel then mostly runs after it.
+//                      kernel while it has work; 0: it keeps them (default 1).  A
+//                      wide GEMM that keeps every CU takes them first, and the
+//                      narrow kernel then mostly runs after it.
 // hkmoe_set_narrow overrides them.
 struct NarrowConfig {
   int cus, max_rows, share;
@@ -151,7 +151,7 @@ std::mutex g_narrow_mu;
 NarrowConfig& narrow_config_ref() {
   static NarrowConfig cfg = [] {
     NarrowConfig c;
-    c.cus = std::max(0, env_int("HKMOE_NARROW_CUS", 48));
+    c.cus = std::max(0, env_int("HKMOE_NARROW_CUS", 64));
     c.max_rows = std::min(kNarrowRows, std::max(0, env_int("HKMOE_NARROW_MAX", kNarrowRows)));
     c.share = env_int("HKMOE_NARROW_SHARE", 1) != 0;
     return c;
@@ -352,8 +352,10 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
   return check_launch("scatter_kernel");
 }
 
-// narrow_cnt: skip (wide kernel) the list's last *narrow_cnt M tiles; narrow_grid > 0:
-// run the narrow kernel on exactly those tiles instead, with that many workgroups.
+// narrow_cnt: skip (wide kernel) the list's last *narrow_cnt M tiles, and with
+// yield_from > 0 leave CUs >= yield_from to the narrow kernel when it has work;
+// narrow_active > 0: run the narrow kernel on exactly those tiles instead (one
+// workgroup per CU; narrow_active of them while 256x256 tiles exist).
 static int grouped_gemm1_impl(const void* x, const float* x_scale, const int32_t* gather,
                               int32_t gather_div, int64_t x_rows, const void* w13, const float* w13_scale,
                               const int32_t* offsets, const int32_t* mtile_offsets,
@@ -361,7 +363,8 @@ static int grouped_gemm1_impl(const void* x, const float* x_scale, const int32_t
                               int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
                               int w_layout, int out_format, void* h, float* h_aux,
                               int32_t* tile_counters, hkmoe_stream_t stream,
-                              const int32_t* narrow_cnt, int wide_grid, int narrow_grid) {
+                              const int32_t* narrow_cnt, int yield_from, int narrow_active,
+                              int narrow_grid = 0) {
   HK_REQUIRE(x && w13 && offsets && mtile_offsets && h, "grouped_gemm1: null pointer");
   HK_REQUIRE(x_scale && w13_scale, "grouped_gemm1: null scale pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1: bad E=%d", num_experts);
@@ -406,24 +409,26 @@ static int grouped_gemm1_impl(const void* x, const float* x_scale, const int32_t
   p.blk_m_log2 = 1;  // 2 x 16 tile blocks
   p.tile_ctr = tile_counters;
   p.narrow_cnt = narrow_cnt;
+  p.yield_from = yield_from;
+  p.narrow_active = narrow_active;
   auto s = static_cast<hipStream_t>(stream);
-  if (narrow_grid > 0) {
+  if (narrow_active > 0) {
     if (scale_mode != HKMOE_SCALE_BLOCK || out_format != HKMOE_E4M3 || narrow_cnt == nullptr ||
-        mtile_list == nullptr)
+        mtile_list == nullptr || tile_counters == nullptr)
       return fail(HKMOE_ERR_INVALID_ARGUMENT, "grouped_gemm1: the narrow kernel needs block scales, "
-                                              "e4m3 output and the M-tile list");
+                                              "e4m3 output, the M-tile list and an item counter");
     p.c_scale = h_aux;
-    return launch_narrow<Epi::kSiluQuant>(p, s, narrow_grid);
+    return launch_narrow<Epi::kSiluQuant>(p, s, narrow_grid > 0 ? narrow_grid : narrow_active);
   }
   if (scale_mode == HKMOE_SCALE_TENSOR) {
     p.amax = h_aux;
-    return launch_gemm<Epi::kSiluBf16, Scale::kTensor>(p, s, wide_grid);
+    return launch_gemm<Epi::kSiluBf16, Scale::kTensor>(p, s);
   }
   if (out_format == HKMOE_E4M3) {
     p.c_scale = h_aux;
-    return launch_gemm<Epi::kSiluQuant, Scale::kBlock>(p, s, wide_grid);
+    return launch_gemm<Epi::kSiluQuant, Scale::kBlock>(p, s);
   }
-  return launch_gemm<Epi::kSiluBf16, Scale::kBlock>(p, s, wide_grid);
+  return launch_gemm<Epi::kSiluBf16, Scale::kBlock>(p, s);
 }
 
 int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gather,
@@ -465,7 +470,8 @@ static int grouped_gemm2_impl(const void* hq, const float* hs, const void* w2, c
                               const int32_t* mtile_list, int64_t rows,
                               int32_t num_experts, int32_t hidden, int32_t inter, int scale_mode,
                               int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream,
-                              const int32_t* narrow_cnt, int wide_grid, int narrow_grid) {
+                              const int32_t* narrow_cnt, int yield_from, int narrow_active,
+                              int narrow_grid = 0) {
   HK_REQUIRE(hq && hs && w2 && w2_scale && offsets && mtile_offsets && y, "grouped_gemm2: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2: hidden=%d must be a multiple of 256", hidden);
@@ -500,15 +506,18 @@ static int grouped_gemm2_impl(const void* hq, const float* hs, const void* w2, c
   p.blk_m_log2 = 1;  // 2 x 16 tile blocks
   p.tile_ctr = tile_counters;
   p.narrow_cnt = narrow_cnt;
+  p.yield_from = yield_from;
+  p.narrow_active = narrow_active;
   auto s = static_cast<hipStream_t>(stream);
-  if (narrow_grid > 0) {
-    if (scale_mode != HKMOE_SCALE_BLOCK || narrow_cnt == nullptr || mtile_list == nullptr)
-      return fail(HKMOE_ERR_INVALID_ARGUMENT, "grouped_gemm2: the narrow kernel needs block scales "
-                                              "and the M-tile list");
-    return launch_narrow<Epi::kStoreBf16>(p, s, narrow_grid);
+  if (narrow_active > 0) {
+    if (scale_mode != HKMOE_SCALE_BLOCK || narrow_cnt == nullptr || mtile_list == nullptr ||
+        tile_counters == nullptr)
+      return fail(HKMOE_ERR_INVALID_ARGUMENT, "grouped_gemm2: the narrow kernel needs block scales, "
+                                              "the M-tile list and an item counter");
+    return launch_narrow<Epi::kStoreBf16>(p, s, narrow_grid > 0 ? narrow_grid : narrow_active);
   }
-  return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kStoreBf16, Scale::kBlock>(p, s, wide_grid)
-                                         : launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s, wide_grid);
+  return scale_mode == HKMOE_SCALE_BLOCK ? launch_gemm<Epi::kStoreBf16, Scale::kBlock>(p, s)
+                                         : launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s);
 }
 
 int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const float* w2_scale,
@@ -532,9 +541,11 @@ int hkmoe_grouped_gemm1_part(const void* x, const float* x_scale, const int32_t*
   HK_REQUIRE(part == 0 || narrow_depth(hidden / kBK) > 0,
              "grouped_gemm1_part: the narrow kernel needs an even number of 128-wide K steps (H=%d)", hidden);
   if (part == 1) {
+    // the narrow kernel's item counter: narrow_info[1], zeroed by hkmoe_expert_offsets_narrow
     return grouped_gemm1_impl(x, x_scale, gather, gather_div, x_rows, w13, w13_scale, offsets, mtile_offsets,
                               mtile_list, rows, num_experts, hidden, inter, HKMOE_SCALE_BLOCK, w_layout,
-                              HKMOE_E4M3, hq, hs, nullptr, stream, narrow_info, 0, grid > 0 ? grid : device_cus());
+                              HKMOE_E4M3, hq, hs, const_cast<int32_t*>(narrow_info) + 1, stream, narrow_info, 0,
+                              grid > 0 ? grid : device_cus());
   }
   return grouped_gemm1_impl(x, x_scale, gather, gather_div, x_rows, w13, w13_scale, offsets, mtile_offsets,
                             mtile_list, rows, num_experts, hidden, inter, HKMOE_SCALE_BLOCK, w_layout, HKMOE_E4M3,
@@ -551,8 +562,10 @@ int hkmoe_grouped_gemm2_part(const void* hq, const float* hs, const void* w2, co
   HK_REQUIRE(grid >= 0 && grid <= 65536, "grouped_gemm2_part: bad grid %d", grid);
   HK_REQUIRE(part == 0 || narrow_depth(inter / kBK) > 0,
              "grouped_gemm2_part: the narrow kernel needs an even number of 128-wide K steps (I=%d)", inter);
+  // the narrow kernel's item counter: narrow_info[2], zeroed by hkmoe_expert_offsets_narrow
   return grouped_gemm2_impl(hq, hs, w2, w2_scale, offsets, mtile_offsets, mtile_list, rows, num_experts, hidden,
-                            inter, HKMOE_SCALE_BLOCK, w_layout, y, part == 1 ? nullptr : tile_counters, stream,
+                            inter, HKMOE_SCALE_BLOCK, w_layout, y,
+                            part == 1 ? const_cast<int32_t*>(narrow_info) + 2 : tile_counters, stream,
                             narrow_info, part == 0 ? grid : 0, part == 1 ? (grid > 0 ? grid : device_cus()) : 0);
 }
 
@@ -712,22 +725,32 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
     // fork: both GEMMs of the narrow experts on the auxiliary stream, enqueued
     // first so that their workgroups find free CUs; join before the combine
     const int ncus = std::min(nc.cus, device_cus());
-    if (hipEventRecord(aux->fork, s) != hipSuccess || hipStreamWaitEvent(aux->aux, aux->fork, 0) != hipSuccess)
+    // Which workgroups work is decided on the device from narrow_info: with
+    // experts of both kinds the narrow kernels use ncus workgroups and (share)
+    // the first 256x256 GEMM leaves them those CUs; with one kind only, that
+    // kind gets every CU it was launched on.
+    if (hipEventRecord(aux->fork, s) != hipSuccess)
+      return fail(HKMOE_ERR_HIP, "moe_forward: fork event failed");
+    const int yield_from = nc.share ? std::max(1, device_cus() - ncus) : 0;
+    if (hipStreamWaitEvent(aux->aux, aux->fork, 0) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: fork to the auxiliary stream failed");
+    // when the average expert fits the narrow kernel (decode-like shapes) it
+    // launches one workgroup per CU and uses them all unless 256x256 tiles
+    // turn out to exist; otherwise it launches ncus workgroups
+    const int ngrid = rows <= static_cast<int64_t>(num_experts) * nc.max_rows ? device_cus() : ncus;
     HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.narrow_info + 1, aux->aux,
-                              w.narrow_info, 0, ncus));
+                              w.narrow_info, 0, ncus, ngrid));
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.narrow_info + 2,
-                              aux->aux, w.narrow_info, 0, ncus));
+                              aux->aux, w.narrow_info, 0, ncus, ngrid));
     if (hipEventRecord(aux->join, aux->aux) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: join event failed");
-    const int wide_grid = nc.share ? std::max(1, device_cus() - ncus) : 0;
     HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream, w.narrow_info,
-                              wide_grid, 0));
+                              yield_from, 0));
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.tile_ctr + 8,
                               stream, w.narrow_info, 0, 0));

@@ -11,8 +11,10 @@
 // CUs run the compute-bound 256x256 tiles of the large experts (the host
 // launches the two kernels on two streams).
 //
-//  * work item: (narrow segment m, 256-row N tile nt); workgroup b takes items
-//    b, b + grid, b + 2*grid, ... (items cost nearly the same).  Segment m is
+//  * work item: (narrow segment m, 256-row N tile nt), taken from one atomic
+//    counter; while the list also holds 256x256 tiles only narrow_active
+//    workgroups take items (the others exit at once and leave their CUs to the
+//    256x256 kernel), else every workgroup of the launch (one per CU) does.  Segment m is
 //    entry first + m of the M-tile list (the narrow experts are listed last).
 //  * 8 waves; wave w owns 32 weight rows = two 16-row fragments:
 //      gate/up GEMM: gate rows 16w..16w+15 of the tile's 128 and the matching
@@ -55,8 +57,8 @@ constexpr int kNarrowCtLd = 128 + 8;                              // staged h ro
 constexpr int kNarrowVmPerStep = 7;
 
 constexpr int narrow_lds_bytes(int P) {
-  // ring, h staging tile, per-wave gathered row indices
-  return (P + 1) * kNarrowStage + kNarrowRows * kNarrowCtLd * 2 + 8 * 256;
+  // ring, h staging tile, per-wave gathered row indices, published item index
+  return (P + 1) * kNarrowStage + kNarrowRows * kNarrowCtLd * 2 + 8 * 256 + 16;
 }
 static_assert(narrow_lds_bytes(8) <= 160 * 1024, "LDS budget");
 
@@ -116,6 +118,10 @@ __device__ __forceinline__ int lds_read_i32(uint32_t a) {
   return v;
 }
 
+__device__ __forceinline__ void lds_write_i32(uint32_t a, int v) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+
 __device__ __forceinline__ void lds_write_b64(uint32_t a, uint2 v) {
   asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(v) : "memory");
 }
@@ -163,8 +169,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   const int n_narrow = sload_i32(p.narrow_cnt, 0);
   const int first = total_mt - n_narrow;
   const int n_items = n_narrow * p.n_tiles;
-  const int grid = gridDim.x;
-  if (static_cast<int>(blockIdx.x) >= n_items) return;
+  // beside 256x256 tiles only narrow_active workgroups take items (the others
+  // exit and leave their CUs to the 256x256 kernel); alone, all of them do
+  const int grid = (first > 0 && p.narrow_active > 0) ? min(p.narrow_active, static_cast<int>(gridDim.x))
+                                                      : static_cast<int>(gridDim.x);
+  if (static_cast<int>(blockIdx.x) >= grid || static_cast<int>(blockIdx.x) >= n_items) return;
+  int32_t* const item_ctr = p.tile_ctr;  // zeroed item counter
+  int* s_q = reinterpret_cast<int*>(gidx + 8 * 64);  // published item index
 
   // this wave's two fragment rows, tile-local (row R of the 256-row tile;
   // fragment R/16 of the packed block) and relative to the N tile's first
@@ -214,6 +225,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   const uint32_t sa_off = kNarrowAScale + 256 * wave + l16 * 4;
   const uint32_t sb_off = kNarrowWScale + 256 * wave;
   const uint32_t gidx_wave = lds_addr(gidx) + 256 * wave;
+  const uint32_t q_addr = lds_addr(s_q);
 
   // weight-scale DMA: lane 0 the first (gate) block row, the other lanes the
   // second (up) block row of this wave's columns, at K block kt
@@ -295,10 +307,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   };
 
   // ---- first item --------------------------------------------------------
-  int it_cur = blockIdx.x;
+  // Items come from one atomic counter, so workgroups that start late (their
+  // CUs were busy) simply take fewer.  Thread 0 fetches the index after next
+  // as soon as it publishes one; its result is first needed an item later.
+  int nxt = 0;
+  if (tid == 0) {
+    lds_write_i32(q_addr, atomicAdd(item_ctr, 1));
+    nxt = atomicAdd(item_ctr, 1);
+  }
+  lds_barrier();
+  const int it_first = __builtin_amdgcn_readfirstlane(lds_read_i32(q_addr));
+  lds_barrier();  // every wave has read the slot before it is rewritten
+  if (it_first >= n_items) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
   Load L, Ln;
   Item C, Cn;
-  decode_head(it_cur, L, C);
+  decode_head(it_first, L, C);
   if (p.a_gather) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // own gather DMA
   decode_tail(L, C);
   i32x8 wbuf[P][2];
@@ -326,6 +352,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
 
     for (int g = 0; g < groups; ++g) {
       const bool last_group = (g == groups - 1);
+      if (g == dgroup && tid == 0) lds_write_i32(q_addr, nxt);  // read after the barrier below
 #pragma unroll
       for (int s = 0; s < P; ++s) {
         const int kt = g * P + s;
@@ -335,9 +362,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
         wait_vm_barrier<kNarrowVmPerStep * (P - 1)>();
         __builtin_amdgcn_sched_barrier(0);
         if (s == 0 && g == dgroup) {
-          have_next = it_cur + grid < n_items;
+          const int it = __builtin_amdgcn_readfirstlane(lds_read_i32(q_addr));
+          have_next = it < n_items;
           if (have_next) {
-            decode_head(it_cur + grid, Ln, Cn);
+            decode_head(it, Ln, Cn);
+            if (tid == 0) nxt = atomicAdd(item_ctr, 1);
           } else {
             Ln = L;
             Cn = C;
@@ -468,7 +497,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
       // the staging tile is next written after at least P more barriers
     }
     if (!have_next) break;
-    it_cur += grid;
     L = Ln;
     C = Cn;
   }

@@ -30,6 +30,9 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # fp32 '/' must be IEEE-correctly rounded (quantisation is bit-exact)
     "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # one-thread queue atomics stay plain atomics: the wave-level rewrite reads
+    # the result right away, which waits for every load in flight
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -180,12 +180,15 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
  *     writes their count to narrow_info[0] and zeroes narrow_info[1..2]
  *     (narrow_info: 3 int32 of device memory).
  *   hkmoe_grouped_gemm{1,2}_part: part 0 runs the 256x256 kernel on the list
- *     without those experts (grid 0: one workgroup per CU, else `grid`); part 1
- *     runs the narrow kernel on exactly those experts with `grid` workgroups
- *     (0: one per CU) and takes no tile counters; its K steps per item (H/128,
- *     I/128) must be even.  The two parts write disjoint rows and may run
- *     concurrently on two streams; together they give the bits of
- *     hkmoe_grouped_gemm{1,2}.
+ *     without those experts, one workgroup per CU; when narrow experts exist,
+ *     its workgroups from `grid` on exit at once and leave their CUs to part 1
+ *     (grid 0: none do).  Part 1 runs the narrow kernel on exactly those
+ *     experts with `grid` workgroups (0: one per CU); its item counter is
+ *     narrow_info[1] for GEMM 1 and [2] for GEMM 2, so it runs once per
+ *     hkmoe_expert_offsets_narrow (tile_counters is not used), and its K steps
+ *     per item, H/128 or I/128, must be even.  The two parts write disjoint
+ *     rows and may run concurrently on two streams;
+ *     together they give the bits of hkmoe_grouped_gemm{1,2}.
  * No reference counterpart (the reference has no grouped GEMM).
  */
 int hkmoe_expert_offsets_narrow(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
@@ -252,7 +255,7 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
  * while the caller's stream is being captured into a graph (the auxiliary
  * stream is created on the first call that is not captured).  Defaults come
  * from HKMOE_NARROW_CUS, HKMOE_NARROW_MAX and HKMOE_NARROW_SHARE in the
- * environment, else 48, 64 and 1.  Concurrent hkmoe_moe_forward calls on one
+ * environment, else 64, 64 and 1.  Concurrent hkmoe_moe_forward calls on one
  * device enqueue their fork/join one at a time (a mutex).
  * No reference counterpart: the reference has no grouped GEMM.
  */

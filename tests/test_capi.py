@@ -106,6 +106,32 @@ def test_grouped_gemm_format_errors(lib):
     assert rc == 1 and "w_layout" in _err(lib)
 
 
+def test_narrow_split_argument_errors(lib):
+    """The narrow split entry points reject bad arguments on the host (before
+    any launch): no narrow_info or M-tile list, a bad part, odd K-step counts,
+    a row threshold above 64 and out-of-range settings."""
+    fake = ctypes.c_void_p(0x1000)
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    g1 = lambda ni, ml, part, hidden: lib.hkmoe_grouped_gemm1_part(
+        fake, fake, fake, i32(2), i64(64), fake, fake, fake, fake, ml, i64(128), i32(8), i32(hidden), i32(128),
+        1, fake, fake, None, ni, i32(part), i32(0), None)
+    assert g1(None, fake, 1, 256) == 1 and "narrow_info" in _err(lib)
+    assert g1(fake, None, 1, 256) == 1 and "mtile_list" in _err(lib)
+    assert g1(fake, fake, 2, 256) == 1 and "part=2" in _err(lib)
+    assert g1(fake, fake, 1, 384) == 1 and "H=384" in _err(lib)
+    rc = lib.hkmoe_grouped_gemm2_part(fake, fake, fake, fake, fake, fake, fake, i64(128), i32(8), i32(256),
+                                      i32(384), 1, fake, None, fake, i32(1), i32(0), None)
+    assert rc == 1 and "I=384" in _err(lib)
+    rc = lib.hkmoe_expert_offsets_narrow(fake, i64(64), i32(8), fake, fake, fake, fake, fake, None, None,
+                                         i32(65), fake, None)
+    assert rc == 1 and "narrow_max=65" in _err(lib)
+    assert lib.hkmoe_set_narrow(i32(-1), i32(64), i32(0)) == 1
+    assert lib.hkmoe_set_narrow(i32(8), i32(65), i32(0)) == 1
+    c, r, w = i32(), i32(), i32()
+    assert lib.hkmoe_get_narrow(ctypes.byref(c), ctypes.byref(r), ctypes.byref(w)) == 0
+    assert 0 <= c.value and 0 <= r.value <= 64
+
+
 def test_pack_weights_argument_errors(lib):
     fake, other = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000)
     i64, i32 = ctypes.c_int64, ctypes.c_int32
