@@ -391,15 +391,20 @@ def _kernel_label(name, dense=False):
             return "gemm"
         epi = name.split("Epi)")[1][0] if "Epi)" in name else "?"
         return "grouped_gemm1" if epi in "234" else "grouped_gemm2"
+    if "gemm_fp8_narrow" in name:
+        epi = name.split("Epi)")[1][0] if "Epi)" in name else "?"
+        return "narrow_gemm1" if epi == "3" else "narrow_gemm2"
     n = name[len("void "):] if name.startswith("void ") else name  # template kernels
     if n.startswith("hkmoe::"):
         return n[len("hkmoe::"):].split("(")[0].split("<")[0].replace("_kernel", "")
     return None
 
 
-def _algorithmic_bytes(cfg, active):
+def _algorithmic_bytes(cfg, active, narrow=None):
     """Compulsory HBM bytes per launch (inputs read once, outputs written once;
-    weights of the `active` experts only)."""
+    weights of the `active` experts only).  With the narrow split (``narrow`` =
+    the bench line's narrow object) the 256x256 GEMMs count the other experts and
+    rows, the narrow GEMMs the narrow ones."""
     if "M" in cfg:  # dense GEMM: A, B, their scales, C
         M, N, K = cfg["M"], cfg["N"], cfg["K"]
         sc = (M + N) * (K // 32) if cfg["mx"] else 8
@@ -413,9 +418,19 @@ def _algorithmic_bytes(cfg, active):
         sc_x = rows * (H // 128) * 4 if cfg["block"] else 4
         sc_h = rows * (I // 128) * 4 if cfg["block"] else 4
         sw1 = sw2 = 0
+    comb = rows * H * 2 + T * H * 2 + rows * 8
+    if narrow:
+        ne, nr = narrow["experts"], narrow["rows"]
+        we, wr = active - ne, rows - nr
+        per_row_x = H + (H // 128) * 4
+        per_row_h = I + (I // 128) * 4
+        return {"grouped_gemm1": we * 2 * I * H + min(T, wr) * per_row_x + wr * per_row_h,
+                "narrow_gemm1": ne * 2 * I * H + nr * per_row_x + nr * per_row_h,
+                "grouped_gemm2": we * H * I + wr * per_row_h + wr * H * 2,
+                "narrow_gemm2": ne * H * I + nr * per_row_h + nr * H * 2,
+                "combine": comb}
     g1 = active * 2 * I * H + sw1 + T * H + sc_x + rows * I + sc_h
     g2 = active * H * I + sw2 + rows * I + sc_h + rows * H * 2
-    comb = rows * H * 2 + T * H * 2 + rows * 8
     return {"grouped_gemm1": g1, "grouped_gemm2": g2, "combine": comb}
 
 
@@ -487,7 +502,7 @@ def summarize_profile(args):
         line = [ln for ln in f if ln.startswith("{")][-1]
     bench = json.loads(line)
     active = bench["config"].get("active_experts", 1)
-    algo = _algorithmic_bytes(cfg, active)
+    algo = _algorithmic_bytes(cfg, active, bench.get("narrow"))
     traffic = {}
     with open(os.path.join(out_dir, f"{name}_traffic.md"), "w") as f:
         f.write(f"# HBM traffic per launch: {what}, workload `{args.config}`\n\n")
@@ -516,6 +531,11 @@ def summarize_profile(args):
             f.write(f"\nAlgorithmic bytes: operands read once, outputs written once, weights of the "
                     f"{active} active experts only (activations e4m3, intermediates e4m3 + fp32 group "
                     f"scales, y and out bf16).\n")
+            if bench.get("narrow"):
+                nw = bench["narrow"]
+                f.write(f"The narrow kernels count the {nw['experts']} experts of at most {nw['max_rows']} rows "
+                        f"({nw['rows']} rows, gathered x rows read once each); the 256x256 GEMMs the other "
+                        f"{active - nw['experts']} experts (GEMM 1: x read once, at most T rows).\n")
     tj = os.path.join(out_dir, "traffic.json")
     old = {}
     if os.path.exists(tj):
