@@ -237,7 +237,8 @@ def narrow_setting(inp):
     cus, max_rows, share = tk_kernel.get_narrow()
     hidden = inp["x_q"].shape[1]
     inter = inp["w2_q"].shape[2]
-    if inp["x_scale"].dim() != 2 or cus <= 0 or max_rows <= 0 or (hidden // 128) % 2 or (inter // 128) % 2:
+    steps = (hidden // 128, inter // 128)
+    if inp["x_scale"].dim() != 2 or cus <= 0 or max_rows <= 0 or any(n % 2 or n > 64 for n in steps):
         return None
     return cus, max_rows, share
 

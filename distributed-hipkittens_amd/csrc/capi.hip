@@ -99,8 +99,10 @@ int launch_gemm(GemmParams p, hipStream_t stream, int grid_override = 0) {
 }
 
 // Prefetch depth of the narrow kernel for K / 128 steps: the largest of 8, 4,
-// 2 that divides the step count (0: the narrow path cannot run this K).
+// 2 that divides the step count (0: the narrow path cannot run this K: an odd
+// step count, or more than 64 steps).
 int narrow_depth(int k_steps) {
+  if (k_steps > kNarrowMaxSteps) return 0;  // an item's scales must fit one LDS buffer
   return k_steps % 8 == 0 ? 8 : k_steps % 4 == 0 ? 4 : k_steps % 2 == 0 ? 2 : 0;
 }
 
@@ -539,13 +541,13 @@ int hkmoe_grouped_gemm1_part(const void* x, const float* x_scale, const int32_t*
   HK_REQUIRE(part == 0 || part == 1, "grouped_gemm1_part: part=%d must be 0 (wide) or 1 (narrow)", part);
   HK_REQUIRE(grid >= 0 && grid <= 65536, "grouped_gemm1_part: bad grid %d", grid);
   HK_REQUIRE(part == 0 || narrow_depth(hidden / kBK) > 0,
-             "grouped_gemm1_part: the narrow kernel needs an even number of 128-wide K steps (H=%d)", hidden);
+             "grouped_gemm1_part: the narrow kernel needs an even number of at most 64 128-wide K steps (H=%d)", hidden);
   if (part == 1) {
     // the narrow kernel's item counter: narrow_info[1], zeroed by hkmoe_expert_offsets_narrow
     return grouped_gemm1_impl(x, x_scale, gather, gather_div, x_rows, w13, w13_scale, offsets, mtile_offsets,
                               mtile_list, rows, num_experts, hidden, inter, HKMOE_SCALE_BLOCK, w_layout,
                               HKMOE_E4M3, hq, hs, const_cast<int32_t*>(narrow_info) + 1, stream, narrow_info, 0,
-                              grid > 0 ? grid : device_cus());
+                              grid > 0 ? grid : device_cus(), device_cus());
   }
   return grouped_gemm1_impl(x, x_scale, gather, gather_div, x_rows, w13, w13_scale, offsets, mtile_offsets,
                             mtile_list, rows, num_experts, hidden, inter, HKMOE_SCALE_BLOCK, w_layout, HKMOE_E4M3,
@@ -561,12 +563,13 @@ int hkmoe_grouped_gemm2_part(const void* hq, const float* hs, const void* w2, co
   HK_REQUIRE(part == 0 || part == 1, "grouped_gemm2_part: part=%d must be 0 (wide) or 1 (narrow)", part);
   HK_REQUIRE(grid >= 0 && grid <= 65536, "grouped_gemm2_part: bad grid %d", grid);
   HK_REQUIRE(part == 0 || narrow_depth(inter / kBK) > 0,
-             "grouped_gemm2_part: the narrow kernel needs an even number of 128-wide K steps (I=%d)", inter);
+             "grouped_gemm2_part: the narrow kernel needs an even number of at most 64 128-wide K steps (I=%d)", inter);
   // the narrow kernel's item counter: narrow_info[2], zeroed by hkmoe_expert_offsets_narrow
   return grouped_gemm2_impl(hq, hs, w2, w2_scale, offsets, mtile_offsets, mtile_list, rows, num_experts, hidden,
                             inter, HKMOE_SCALE_BLOCK, w_layout, y,
                             part == 1 ? const_cast<int32_t*>(narrow_info) + 2 : tile_counters, stream,
-                            narrow_info, part == 0 ? grid : 0, part == 1 ? (grid > 0 ? grid : device_cus()) : 0);
+                            narrow_info, part == 0 ? grid : 0, part == 1 ? (grid > 0 ? grid : device_cus()) : 0,
+                            part == 1 ? device_cus() : 0);
 }
 
 int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k, int32_t gate_up,
@@ -616,7 +619,8 @@ struct MoeWorkspace {
   int32_t* mtile_list;  // [M tiles][2], at most ceil(T*k/256) + E tiles
   float* amax;
   int32_t* tile_ctr;  // HKMOE_TILE_COUNTERS
-  int32_t* narrow_info;  // [0] narrow M tiles, [1] / [2] narrow item counters of GEMM 1 / 2
+  int32_t* narrow_info;  // [0] narrow M tiles, [1] / [2] narrow item counters of GEMM 1 / 2,
+                         // [3] / [4] their active-slot counters
   int32_t* perm;
   int32_t* inv_perm;
   uint16_t* h;   // per-tensor mode only: bf16 intermediate before requantisation
@@ -653,7 +657,7 @@ MoeWorkspace carve(uint8_t* base, int64_t t, int32_t e, int32_t k, int32_t hidde
   w.mtile_list = reinterpret_cast<int32_t*>(take(((r + kBM - 1) / kBM + e) * 8));
   w.amax = reinterpret_cast<float*>(take(4));
   w.tile_ctr = reinterpret_cast<int32_t*>(take(HKMOE_TILE_COUNTERS * 4));
-  w.narrow_info = reinterpret_cast<int32_t*>(take((1 + kNarrowCounters) * 4));
+  w.narrow_info = reinterpret_cast<int32_t*>(take((1 + kNarrowCounters) * 4));  // HKMOE_NARROW_INFO ints
   w.perm = reinterpret_cast<int32_t*>(take(r * 4));
   w.inv_perm = reinterpret_cast<int32_t*>(take(r * 4));
   const int64_t ws = mx_words_per_step(r, e);
@@ -734,10 +738,9 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
     const int yield_from = nc.share ? std::max(1, device_cus() - ncus) : 0;
     if (hipStreamWaitEvent(aux->aux, aux->fork, 0) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: fork to the auxiliary stream failed");
-    // when the average expert fits the narrow kernel (decode-like shapes) it
-    // launches one workgroup per CU and uses them all unless 256x256 tiles
-    // turn out to exist; otherwise it launches ncus workgroups
-    const int ngrid = rows <= static_cast<int64_t>(num_experts) * nc.max_rows ? device_cus() : ncus;
+    // the narrow kernels launch one workgroup per CU: beside 256x256 tiles the
+    // first ncus to start take items, else all of them (decode-like shapes)
+    const int ngrid = device_cus();
     HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.narrow_info + 1, aux->aux,

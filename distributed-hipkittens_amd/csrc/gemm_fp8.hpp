@@ -95,7 +95,8 @@ struct GemmParams {
   const int32_t* mtile_list;   // optional [M tiles][2] = (expert, first row), in schedule order
   float* amax;                 // kSiluBf16: running max |h| (uint-ordered), may be null
   int32_t* tile_ctr;           // optional: 8 zeroed per-XCD tile counters (dynamic schedule)
-                               // (narrow kernel: one zeroed item counter)
+                               // (narrow kernel: zeroed item counter at [0], active-slot
+                               // counter at [2])
   const int32_t* narrow_cnt;   // optional: the last *narrow_cnt M-tile list entries belong to
                                // the narrow kernel (gemm_narrow.hpp); this kernel skips them
   int32_t yield_from;          // > 0: with narrow tiles present, workgroups >= yield_from exit

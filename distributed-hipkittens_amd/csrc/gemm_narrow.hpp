@@ -13,8 +13,9 @@
 //
 //  * work item: (narrow segment m, 256-row N tile nt), taken from one atomic
 //    counter; while the list also holds 256x256 tiles only narrow_active
-//    workgroups take items (the others exit at once and leave their CUs to the
-//    256x256 kernel), else every workgroup of the launch (one per CU) does.  Segment m is
+//    workgroups take items, the first ones to start (a second counter), and
+//    the others exit at once and leave their CUs to the 256x256 kernel; else
+//    every workgroup of the launch (one per CU) does.  Segment m is
 //    entry first + m of the M-tile list (the narrow experts are listed last).
 //  * 8 waves; wave w owns 32 weight rows = two 16-row fragments:
 //      gate/up GEMM: gate rows 16w..16w+15 of the tile's 128 and the matching
@@ -25,14 +26,16 @@
 //    LDS: the MFMA operands, the rescale arithmetic and the epilogue are those
 //    of the 256x256 kernel, so both kernels give the same bits.
 //  * activations: every wave DMAs 8 of the segment's 64 rows (rows past the
-//    segment repeat its last row) into an LDS ring of P+1 stages, and its own
-//    copy of the 64 row scales and of its two weight scales (all lanes active,
-//    so the compiler counts every load), loaded P steps ahead like the
-//    weights; one barrier per K step.
-//  * every wave issues exactly 7 vector-memory instructions per K step (A rows,
-//    A scales, weight scales, 4 weight loads), so "step kt has landed" is
-//    vmcnt(7*(P-1)); after the last item the loads continue on that item's
-//    first steps (valid addresses, never read), so the count never changes.
+//    segment repeat its last row) into an LDS ring of P+1 stages, loaded P
+//    steps ahead like the weights; one barrier per K step.  An item's
+//    activation and weight scales for all its K steps are DMA'd into one of two
+//    LDS buffers once, when the item is decoded (at least P steps before its
+//    first step).
+//  * every wave issues exactly 5 vector-memory instructions per K step (A rows,
+//    4 weight loads), so "step kt has landed" is vmcnt(5*(P-1)) (other loads
+//    only add to the count, so the wait can only be longer); after the last
+//    item the loads continue on that item's first steps (valid addresses, never
+//    read), so the count never changes.
 //  * K steps per item must be a multiple of P, so a group of P unrolled steps
 //    never straddles two items; the loads of an item's last group are the next
 //    item's first P steps.
@@ -50,15 +53,22 @@ namespace hkmoe {
 
 constexpr int kNarrowRows = 64;
 constexpr int kNarrowAStage = kNarrowRows * kBK;                  // 8 KiB of A rows
-constexpr int kNarrowAScale = kNarrowAStage;                      // per wave: the 64 row scales
-constexpr int kNarrowWScale = kNarrowAScale + 8 * 256;             // per wave: its 2 weight scales
-constexpr int kNarrowStage = kNarrowWScale + 8 * 256;
+constexpr int kNarrowStage = kNarrowAStage;                       // one ring stage: A rows
+constexpr int kNarrowMaxSteps = 64;                               // K <= 8192
+// per-item scales, two buffers (current / next item): [K step][64 rows] activation
+// scales, then per wave [2 block rows][K step] weight scales
+constexpr int kNarrowWsOff = kNarrowMaxSteps * kNarrowRows * 4;  // 16 KiB
+constexpr int kNarrowScaleBuf = kNarrowWsOff + 8 * 2 * kNarrowMaxSteps * 4;
 constexpr int kNarrowCtLd = 128 + 8;                              // staged h row (bf16)
-constexpr int kNarrowVmPerStep = 7;
+constexpr int kNarrowVmPerStep = 5;
 
+constexpr int narrow_ct_off(int P) { return (P + 1) * kNarrowStage; }
+constexpr int narrow_gidx_off(int P) { return narrow_ct_off(P) + kNarrowRows * kNarrowCtLd * 2; }
+constexpr int narrow_q_off(int P) { return narrow_gidx_off(P) + 8 * 256; }
+constexpr int narrow_scale_off(int P) { return narrow_q_off(P) + 256; }
 constexpr int narrow_lds_bytes(int P) {
-  // ring, h staging tile, per-wave gathered row indices, published item index
-  return (P + 1) * kNarrowStage + kNarrowRows * kNarrowCtLd * 2 + 8 * 256 + 16;
+  // ring, h staging tile, per-wave gathered row indices, published item index, scales
+  return narrow_scale_off(P) + 2 * kNarrowScaleBuf;
 }
 static_assert(narrow_lds_bytes(8) <= 160 * 1024, "LDS budget");
 
@@ -112,6 +122,15 @@ __device__ __forceinline__ float2 lds_read_f2(uint32_t a) {
   return v;
 }
 
+// the dwords at a and a + 256 (an item's two weight-scale rows at one K step)
+__device__ __forceinline__ float2 lds_read_w2(uint32_t a) {
+  float x, y;
+  asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:256\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(x), "=&v"(y)
+               : "v"(a));
+  return float2{x, y};
+}
+
 __device__ __forceinline__ int lds_read_i32(uint32_t a) {
   int v;
   asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
@@ -153,8 +172,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   constexpr bool kSilu = (EPI == Epi::kSiluQuant);
   constexpr int kRing = P + 1;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  uint16_t* ct = reinterpret_cast<uint16_t*>(smem + kRing * kNarrowStage);
-  int32_t* gidx = reinterpret_cast<int32_t*>(smem + kRing * kNarrowStage + kNarrowRows * kNarrowCtLd * 2);
+  uint16_t* ct = reinterpret_cast<uint16_t*>(smem + narrow_ct_off(P));
+  int32_t* gidx = reinterpret_cast<int32_t*>(smem + narrow_gidx_off(P));
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -171,11 +190,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   const int n_items = n_narrow * p.n_tiles;
   // beside 256x256 tiles only narrow_active workgroups take items (the others
   // exit and leave their CUs to the 256x256 kernel); alone, all of them do
-  const int grid = (first > 0 && p.narrow_active > 0) ? min(p.narrow_active, static_cast<int>(gridDim.x))
-                                                      : static_cast<int>(gridDim.x);
-  if (static_cast<int>(blockIdx.x) >= grid || static_cast<int>(blockIdx.x) >= n_items) return;
-  int32_t* const item_ctr = p.tile_ctr;  // zeroed item counter
-  int* s_q = reinterpret_cast<int*>(gidx + 8 * 64);  // published item index
+  if (n_items <= 0) return;
+  int32_t* const item_ctr = p.tile_ctr;  // zeroed item counter; p.tile_ctr[2]: active slots
+  int* s_q = reinterpret_cast<int*>(smem + narrow_q_off(P));  // published item index
 
   // this wave's two fragment rows, tile-local (row R of the 256-row tile;
   // fragment R/16 of the packed block) and relative to the N tile's first
@@ -222,14 +239,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   const uint32_t smem_base = lds_addr(smem);
   const uint32_t lo_off = l16 * kBK + (((2 * lg) ^ fx) << 4);
   const uint32_t hi_off = l16 * kBK + (((2 * lg + 1) ^ fx) << 4);
-  const uint32_t sa_off = kNarrowAScale + 256 * wave + l16 * 4;
-  const uint32_t sb_off = kNarrowWScale + 256 * wave;
+  const uint32_t scale_base = smem_base + narrow_scale_off(P);
+  const uint32_t sa_lane = l16 * 4;                              // + buffer + kt*256 + 64*i
+  const uint32_t sb_wave = kNarrowWsOff + wave * 2 * kNarrowMaxSteps * 4;  // + buffer + h*256 + kt*4
   const uint32_t gidx_wave = lds_addr(gidx) + 256 * wave;
   const uint32_t q_addr = lds_addr(s_q);
 
-  // weight-scale DMA: lane 0 the first (gate) block row, the other lanes the
-  // second (up) block row of this wave's columns, at K block kt
-  const int ws_voff = (kSilu && lane >= 1) ? (p.n_out / kGroup) * k_steps * 4 : 0;
+  // weight-scale staging: lane l fetches K block min(l, k_steps-1) of the first
+  // (gate) and of the second (up) block row of this wave's columns
+  const int ws_voff0 = min(lane, k_steps - 1) * 4;
+  const int ws_voff1 = ws_voff0 + (kSilu ? (p.n_out / kGroup) * k_steps * 4 : 0);
   const int kstride = p.b_packed ? kTileBytes : kBK;
 
   // per-item state of the load side: uniform descriptors, and the lane's
@@ -240,7 +259,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   };
   // per-item state of the compute side
   struct Item {
-    int row0, valid, nt, mf;
+    int row0, valid, nt, mf, buf;  // buf: which scale buffer holds its scales
   };
 
   // uniform part of item `it` (scalar loads); with a row gather, the DMA of
@@ -281,24 +300,34 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
     L.as_voff = static_cast<int>(ts * p.as_rs) * 4;
   };
 
-  // the 7 loads of K step kt into ring slot `slot` and weight registers wr
-  auto issue = [&](const Load& L, int kt, int slot, i32x8 (&wr)[2]) {
-    // descriptors and K offsets are wave-uniform: keep them in SGPRs (a
-    // descriptor in VGPRs would turn every load into a waterfall loop)
-    i32x4 srd, ssrd;
-    srd.x = __builtin_amdgcn_readfirstlane(L.wsrd.x);
-    srd.y = __builtin_amdgcn_readfirstlane(L.wsrd.y);
-    srd.z = __builtin_amdgcn_readfirstlane(L.wsrd.z);
-    srd.w = __builtin_amdgcn_readfirstlane(L.wsrd.w);
+  // all K steps' activation and weight scales of item C into its buffer (wave w
+  // fetches the activation scales of K steps w, w+8, ... and its own weight scales)
+  auto stage_scales = [&](const Load& L, const Item& C) {
+    uint8_t* sb = smem + narrow_scale_off(P) + C.buf * kNarrowScaleBuf;
+    for (int kt = wave; kt < k_steps; kt += 8)
+      load_lds_4B(as_srd, sb + kt * (kNarrowRows * 4), L.as_voff, static_cast<int>(kt * p.as_ks) * 4);
+    i32x4 ssrd;
     ssrd.x = __builtin_amdgcn_readfirstlane(L.ssrd.x);
     ssrd.y = __builtin_amdgcn_readfirstlane(L.ssrd.y);
     ssrd.z = __builtin_amdgcn_readfirstlane(L.ssrd.z);
     ssrd.w = __builtin_amdgcn_readfirstlane(L.ssrd.w);
+    uint8_t* wsb = sb + kNarrowWsOff + wave * 2 * kNarrowMaxSteps * 4;
+    load_lds_4B(ssrd, wsb, ws_voff0, 0);
+    load_lds_4B(ssrd, wsb + kNarrowMaxSteps * 4, ws_voff1, 0);
+  };
+
+  // the 5 loads of K step kt into ring slot `slot` and weight registers wr
+  auto issue = [&](const Load& L, int kt, int slot, i32x8 (&wr)[2]) {
+    // descriptors and K offsets are wave-uniform: keep them in SGPRs (a
+    // descriptor in VGPRs would turn every load into a waterfall loop)
+    i32x4 srd;
+    srd.x = __builtin_amdgcn_readfirstlane(L.wsrd.x);
+    srd.y = __builtin_amdgcn_readfirstlane(L.wsrd.y);
+    srd.z = __builtin_amdgcn_readfirstlane(L.wsrd.z);
+    srd.w = __builtin_amdgcn_readfirstlane(L.wsrd.w);
     const int ktu = __builtin_amdgcn_readfirstlane(kt);
     uint8_t* st = smem + __builtin_amdgcn_readfirstlane(slot) * kNarrowStage;
     load_lds_16B(a_srd, st + 8 * wave * kBK, L.a_voff, ktu * kBK);
-    load_lds_4B(as_srd, st + kNarrowAScale + 256 * wave, L.as_voff, static_cast<int>(ktu * p.as_ks) * 4);
-    load_lds_4B(ssrd, st + kNarrowWScale + 256 * wave, ws_voff, ktu * 4);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       wr[j].lo = hk_raw_buffer_load_v4i32(srd, wvoff[2 * j], ktu * kstride, 0);
@@ -310,10 +339,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   // Items come from one atomic counter, so workgroups that start late (their
   // CUs were busy) simply take fewer.  Thread 0 fetches the index after next
   // as soon as it publishes one; its result is first needed an item later.
+  // Beside 256x256 tiles only narrow_active workgroups take items: the first
+  // ones to start (an atomic slot counter), wherever the hardware placed them;
+  // later ones exit and leave their CUs to the 256x256 kernel.
+  const bool limited = first > 0 && p.narrow_active > 0;
   int nxt = 0;
   if (tid == 0) {
-    lds_write_i32(q_addr, atomicAdd(item_ctr, 1));
-    nxt = atomicAdd(item_ctr, 1);
+    int it0 = n_items;  // "no item": exit
+    if (!limited || atomicAdd(item_ctr + 2, 1) < p.narrow_active) {
+      it0 = atomicAdd(item_ctr, 1);
+      nxt = atomicAdd(item_ctr, 1);
+    }
+    lds_write_i32(q_addr, it0);
   }
   lds_barrier();
   const int it_first = __builtin_amdgcn_readfirstlane(lds_read_i32(q_addr));
@@ -324,9 +361,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   }
   Load L, Ln;
   Item C, Cn;
+  C.buf = 0;
   decode_head(it_first, L, C);
   if (p.a_gather) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // own gather DMA
   decode_tail(L, C);
+  stage_scales(L, C);
   i32x8 wbuf[P][2];
 #pragma unroll
   for (int s = 0; s < P; ++s) issue(L, s, s, wbuf[s]);
@@ -365,6 +404,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
           const int it = __builtin_amdgcn_readfirstlane(lds_read_i32(q_addr));
           have_next = it < n_items;
           if (have_next) {
+            Cn.buf = C.buf ^ 1;
             decode_head(it, Ln, Cn);
             if (tid == 0) nxt = atomicAdd(item_ctr, 1);
           } else {
@@ -376,9 +416,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
           // a single-group item decodes and reads its indices in one step
           if (groups == 1 && p.a_gather) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           decode_tail(Ln, Cn);
+          stage_scales(Ln, Cn);
         }
         const uint32_t st = smem_base + __builtin_amdgcn_readfirstlane(cp_slot) * kNarrowStage;
-        const float2 sbv = lds_read_f2(st + sb_off);
+        const uint32_t sbuf = scale_base + C.buf * kNarrowScaleBuf;
+        const uint32_t sa_addr = sbuf + kt * (kNarrowRows * 4) + sa_lane;
+        const float2 sbv = lds_read_w2(sbuf + sb_wave + kt * 4);
         const float sb_cur0 = sbv.x;                   // lane 0's DMA: gate / only block
         const float sb_cur1 = kSilu ? sbv.y : sbv.x;   // lane 1's DMA: up block
         // rescale and MFMAs, in the 256x256 kernel's arithmetic
@@ -391,7 +434,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
           constexpr int i = decltype(i_tag)::value;
           i32x8 af;
           float sa_cur;
-          lds_frag<2048 * i, 64 * i>(st + lo_off, st + hi_off, st + sa_off, af, sa_cur);
+          lds_frag<2048 * i, 64 * i>(st + lo_off, st + hi_off, sa_addr, af, sa_cur);
           const float ra = sa_prev[i] * __builtin_amdgcn_rcpf(sa_cur);
           const float r0 = ra * rb0, r1 = ra * rb1;
           sa_prev[i] = sa_cur;
@@ -409,9 +452,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
         const int ld_slot = cp_slot == 0 ? P : cp_slot - 1;
         Load LL;
         LL.wsrd = last_group ? Ln.wsrd : L.wsrd;
-        LL.ssrd = last_group ? Ln.ssrd : L.ssrd;
         LL.a_voff = last_group ? Ln.a_voff : L.a_voff;
-        LL.as_voff = last_group ? Ln.as_voff : L.as_voff;
         issue(LL, last_group ? s : kt + P, ld_slot, wbuf[s]);
         cp_slot = cp_slot == P ? 0 : cp_slot + 1;
       }

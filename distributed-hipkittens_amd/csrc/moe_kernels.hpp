@@ -19,7 +19,8 @@ constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kScanThreads = 1024;
 constexpr int kTileCounters = 16;  // HKMOE_TILE_COUNTERS
-constexpr int kNarrowCounters = 2;  // narrow kernel item counters (GEMM 1, GEMM 2)
+constexpr int kNarrowCounters = 4;  // narrow kernel item counters (GEMM 1, GEMM 2), then their
+                                    // active-slot counters
 
 __device__ __forceinline__ bool route_better(float av, int ai, float bv, int bi) {
   if (bi < 0) return ai >= 0;

@@ -150,7 +150,7 @@ void dispatch_expert_offsets(py::object bc, int64_t num_tokens, py::object count
                              py::object narrow_info) {
   auto ni = as_tensor_opt(narrow_info, "narrow_info");
   want_dtype(ni, "narrow_info", kI32);
-  if (ni.ptr && ni.numel() < 3) throw std::runtime_error("narrow_info must hold 3 ints");
+  if (ni.ptr && ni.numel() < 5) throw std::runtime_error("narrow_info must hold 5 ints");
   auto b = as_tensor(bc, "block_counts"), c = as_tensor(counts, "counts"),
        o = as_tensor(offsets, "offsets"), bb = as_tensor(block_base, "block_base"),
        mo = as_tensor(mtile_offsets, "mtile_offsets"), am = as_tensor_opt(amax, "amax"),

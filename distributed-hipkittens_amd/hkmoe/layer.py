@@ -203,7 +203,7 @@ def _steps_narrow(r, x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top
     cus, max_rows, share = narrow
     t = x_q.shape[0]
     dev = x_q.device
-    r["narrow_info"] = torch.zeros(3, dtype=torch.int32, device=dev)
+    r["narrow_info"] = torch.zeros(5, dtype=torch.int32, device=dev)
     tk_kernel.dispatch_route_topk(logits, r["topk_idx"], r["topk_w"], r["block_counts"])
     tk_kernel.dispatch_expert_offsets(r["block_counts"], t, r["counts"], r["offsets"],
                                       r["block_base"], r["mtile_offsets"], r["amax"], r["tile_ctr"],

@@ -177,16 +177,18 @@ int hkmoe_grouped_gemm2(const void* hq, const float* hs, const void* w2, const f
  * e4m3 h), for callers that enqueue the parts themselves:
  *   hkmoe_expert_offsets_narrow: hkmoe_expert_offsets that also moves the experts
  *     of 1..narrow_max rows (narrow_max <= 64) to the end of the M-tile list,
- *     writes their count to narrow_info[0] and zeroes narrow_info[1..2]
- *     (narrow_info: 3 int32 of device memory).
+ *     writes their count to narrow_info[0] and zeroes the narrow kernels'
+ *     counters narrow_info[1..4] (narrow_info: 5 int32 of device memory).
  *   hkmoe_grouped_gemm{1,2}_part: part 0 runs the 256x256 kernel on the list
  *     without those experts, one workgroup per CU; when narrow experts exist,
  *     its workgroups from `grid` on exit at once and leave their CUs to part 1
  *     (grid 0: none do).  Part 1 runs the narrow kernel on exactly those
- *     experts with `grid` workgroups (0: one per CU); its item counter is
- *     narrow_info[1] for GEMM 1 and [2] for GEMM 2, so it runs once per
+ *     experts, one workgroup per CU, of which the first `grid` to start take
+ *     items (0: all of them) while the list also holds 256x256 tiles; its
+ *     counters are narrow_info[1] and [3] for GEMM 1, [2] and [4] for GEMM 2,
+ *     so it runs once per
  *     hkmoe_expert_offsets_narrow (tile_counters is not used), and its K steps
- *     per item, H/128 or I/128, must be even.  The two parts write disjoint
+ *     per item, H/128 or I/128, must be even and at most 64.  The two parts write disjoint
  *     rows and may run concurrently on two streams;
  *     together they give the bits of hkmoe_grouped_gemm{1,2}.
  * No reference counterpart (the reference has no grouped GEMM).
@@ -251,7 +253,7 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
  * stream; the caller's stream waits for it before the combine.  Results are
  * bit-identical with the narrow path on or off.  cus == 0 turns it off;
  * wide_share != 0 launches the first wide GEMM on (CUs - cus) workgroups.
- * It also stays off when H/128 or I/128 is odd, and for a first call made
+ * It also stays off when H/128 or I/128 is odd or above 64, and for a first call made
  * while the caller's stream is being captured into a graph (the auxiliary
  * stream is created on the first call that is not captured).  Defaults come
  * from HKMOE_NARROW_CUS, HKMOE_NARROW_MAX and HKMOE_NARROW_SHARE in the

@@ -200,7 +200,7 @@ def test_workspace_size_formula(lib, t, e, k, h, i, block):
     r = t * k
     nblk = (t + 31) // 32
     parts = [r * 4, r * 4, nblk * e * 4, nblk * e * 4, e * 4, (e + 1) * 4, (e + 1) * 4,
-             ((r + 255) // 256 + e) * 8, 4, 16 * 4, 3 * 4, r * 4, r * 4]
+             ((r + 255) // 256 + e) * 8, 4, 16 * 4, 5 * 4, r * 4, r * 4]
     if not block:
         parts.append(r * i * 2)
     parts += [r * i, r * (i // 128) * 4 if block else 4, r * h * 2]
