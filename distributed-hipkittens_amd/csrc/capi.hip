@@ -155,7 +155,7 @@ NarrowConfig& narrow_config_ref() {
     NarrowConfig c;
     c.cus = std::max(0, env_int("HKMOE_NARROW_CUS", 64));
     c.max_rows = std::min(kNarrowRows, std::max(0, env_int("HKMOE_NARROW_MAX", kNarrowRows)));
-    c.share = env_int("HKMOE_NARROW_SHARE", 1) != 0;
+    c.share = std::min(2, std::max(0, env_int("HKMOE_NARROW_SHARE", 1)));
     return c;
   }();
   return cfg;
@@ -221,11 +221,12 @@ int hkmoe_set_narrow(int32_t cus, int32_t max_rows, int32_t wide_share) {
   HK_REQUIRE(cus >= 0 && cus <= 4096, "set_narrow: cus=%d outside [0, 4096]", cus);
   HK_REQUIRE(max_rows >= 0 && max_rows <= kNarrowRows, "set_narrow: max_rows=%d outside [0, %d]", max_rows,
              kNarrowRows);
+  HK_REQUIRE(wide_share >= 0 && wide_share <= 2, "set_narrow: wide_share=%d outside [0, 2]", wide_share);
   std::lock_guard<std::mutex> g(g_narrow_mu);
   NarrowConfig& c = narrow_config_ref();
   c.cus = cus;
   c.max_rows = max_rows;
-  c.share = wide_share != 0;
+  c.share = wide_share;
   return HKMOE_OK;
 }
 
@@ -428,7 +429,7 @@ static int grouped_gemm1_impl(const void* x, const float* x_scale, const int32_t
   }
   if (out_format == HKMOE_E4M3) {
     p.c_scale = h_aux;
-    return launch_gemm<Epi::kSiluQuant, Scale::kBlock>(p, s);
+    return launch_gemm<Epi::kSiluQuant, Scale::kBlock>(p, s, yield_from < 0 ? narrow_grid : 0);
   }
   return launch_gemm<Epi::kSiluBf16, Scale::kBlock>(p, s);
 }
@@ -748,16 +749,29 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.narrow_info + 2,
                               aux->aux, w.narrow_info, 0, ncus, ngrid));
+    // share == 1: once the narrow GEMMs are done, their CUs join the first 256x256
+    // GEMM's tile queues (a second launch of it on the auxiliary stream, which
+    // takes whatever tiles are left); the second 256x256 GEMM then waits for both.
+    // Not when every row fits narrow experts (rows <= E * max_rows, decode-like):
+    // there the extra launch would only lengthen the critical path.
+    const bool late_join = nc.share == 1 && rows > static_cast<int64_t>(num_experts) * nc.max_rows;
+    if (late_join)
+      HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
+                                w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
+                                w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, aux->aux, w.narrow_info,
+                                -1, 0, ncus));
     if (hipEventRecord(aux->join, aux->aux) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: join event failed");
     HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream, w.narrow_info,
                               yield_from, 0));
+    if (late_join && hipStreamWaitEvent(s, aux->join, 0) != hipSuccess)
+      return fail(HKMOE_ERR_HIP, "moe_forward: join of the auxiliary stream failed");
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.tile_ctr + 8,
                               stream, w.narrow_info, 0, 0));
-    if (hipStreamWaitEvent(s, aux->join, 0) != hipSuccess)
+    if (!late_join && hipStreamWaitEvent(s, aux->join, 0) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: join of the auxiliary stream failed");
     aux_lock.unlock();
     HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));

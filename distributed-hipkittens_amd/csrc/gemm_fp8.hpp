@@ -100,7 +100,9 @@ struct GemmParams {
   const int32_t* narrow_cnt;   // optional: the last *narrow_cnt M-tile list entries belong to
                                // the narrow kernel (gemm_narrow.hpp); this kernel skips them
   int32_t yield_from;          // > 0: with narrow tiles present, workgroups >= yield_from exit
-                               // at once (their CUs go to the narrow kernel)
+                               // at once (their CUs go to the narrow kernel);
+                               // < 0: a second launch that joins the tile queues once the
+                               // narrow kernels are done; it exits at once without narrow tiles
   int32_t narrow_active;       // narrow kernel: workgroups that take items while 256x256
                                // tiles exist (0: all); without such tiles, all of them do
   int64_t rows;                // output rows (dense: M)
@@ -240,9 +242,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 
   // leave this CU to the narrow kernel when it has work (device-side decision:
   // the host does not know the expert sizes)
-  if (p.narrow_cnt != nullptr && p.yield_from > 0 && static_cast<int>(blockIdx.x) >= p.yield_from &&
-      __builtin_amdgcn_readfirstlane(*p.narrow_cnt) > 0)
-    return;
+  if (p.narrow_cnt != nullptr && p.yield_from != 0) {
+    const int ncnt = __builtin_amdgcn_readfirstlane(*p.narrow_cnt);
+    if (p.yield_from > 0 ? (ncnt > 0 && static_cast<int>(blockIdx.x) >= p.yield_from) : ncnt == 0) return;
+  }
   const bool dense = (p.offsets == nullptr);
   const int total_mtiles = dense ? static_cast<int>((p.rows + kBM - 1) / kBM)
                                  : __builtin_amdgcn_readfirstlane(p.mtile_offsets[p.num_experts] -

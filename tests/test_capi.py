@@ -127,6 +127,7 @@ def test_narrow_split_argument_errors(lib):
     assert rc == 1 and "narrow_max=65" in _err(lib)
     assert lib.hkmoe_set_narrow(i32(-1), i32(64), i32(0)) == 1
     assert lib.hkmoe_set_narrow(i32(8), i32(65), i32(0)) == 1
+    assert lib.hkmoe_set_narrow(i32(8), i32(64), i32(3)) == 1 and "wide_share=3" in _err(lib)
     c, r, w = i32(), i32(), i32()
     assert lib.hkmoe_get_narrow(ctypes.byref(c), ctypes.byref(r), ctypes.byref(w)) == 0
     assert 0 <= c.value and 0 <= r.value <= 64
