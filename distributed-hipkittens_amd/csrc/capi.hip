@@ -749,12 +749,12 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.narrow_info + 2,
                               aux->aux, w.narrow_info, 0, ncus, ngrid));
-    // share == 1: once the narrow GEMMs are done, their CUs join the first 256x256
+    // share == 2: once the narrow GEMMs are done, their CUs join the first 256x256
     // GEMM's tile queues (a second launch of it on the auxiliary stream, which
     // takes whatever tiles are left); the second 256x256 GEMM then waits for both.
     // Not when every row fits narrow experts (rows <= E * max_rows, decode-like):
     // there the extra launch would only lengthen the critical path.
-    const bool late_join = nc.share == 1 && rows > static_cast<int64_t>(num_experts) * nc.max_rows;
+    const bool late_join = nc.share == 2 && rows > static_cast<int64_t>(num_experts) * nc.max_rows;
     if (late_join)
       HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                                 w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,

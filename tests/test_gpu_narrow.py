@@ -5,7 +5,7 @@ The narrow kernel uses the 256x256 kernel's operand order, rescale arithmetic
 and epilogue, so the layer output is bit-identical with the narrow path off,
 on, on a tiny grid (many items per workgroup), with a lower row threshold, and
 with the narrow path's CUs joining the first 256x256 GEMM's tiles afterwards
-(wide_share 1) or not (2).
+(wide_share 2) or not (1).
 With top-1 routing the combine is the identity (weight 1.0), so ``out`` is
 GEMM 2's output ``y`` itself and those cases pin it bit for bit.  Shapes cover
 prefetch depths 8, 4 and 2, items of one and of several groups of K steps,
@@ -76,11 +76,11 @@ def test_narrow_bit_exact(hk, narrow_restore, name, packed):
     hk.tk_kernel.set_narrow(0, 64, 0)
     off = _one_call(hk, g, w13, w2, packed).clone()
     assert torch.equal(off.view(torch.int16), steps["out"].view(torch.int16))
-    # threshold 16 with wide_share 1: where T*k > 16*E (p8_g2_g1, p4_p2, dsv3_shape)
+    # threshold 16 with wide_share 2: where T*k > 16*E (p8_g2_g1, p4_p2, dsv3_shape)
     # the narrow CUs also join the first 256x256 GEMM's tiles (late join)
     print(f"  experts of 1..16 rows: {int(((counts > 0) & (counts <= 16)).sum())}", flush=True)
     for cus, max_rows, share in ((48, 64, 0), (3, 64, 0), (48, 16, 0), (40, 64, 1), (64, 64, 2), (3, 64, 1),
-                                 (64, 16, 1), (3, 16, 1)):
+                                 (64, 16, 2), (3, 16, 2)):
         hk.tk_kernel.set_narrow(cus, max_rows, share)
         on = _one_call(hk, g, w13, w2, packed)
         assert torch.equal(on.view(torch.int16), off.view(torch.int16)), (cus, max_rows, share)
