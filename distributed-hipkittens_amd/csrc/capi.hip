@@ -196,6 +196,27 @@ int get_aux(hipStream_t main_stream, AuxStreams** out) {
   return HKMOE_OK;
 }
 
+// Workgroups the narrow kernels may take while 256x256 tiles exist: at most
+// three quarters of the CUs, so the first 256x256 GEMM keeps at least a quarter
+// of them whatever hkmoe_set_narrow asked for.
+int narrow_cus_limit(int cus) { return std::min(cus, device_cus() - device_cus() / 4); }
+
+// Joins the auxiliary stream back into the caller's stream when it goes out of
+// scope, unless disarmed: every exit path after the fork (errors included)
+// leaves the caller's stream ordered after the narrow kernels, which read and
+// write the workspace, and a capture with the auxiliary stream joined.
+struct AuxJoin {
+  AuxStreams* a;
+  hipStream_t s;
+  bool armed = true;
+  ~AuxJoin() {
+    if (armed) {
+      (void)hipEventRecord(a->join, a->aux);
+      (void)hipStreamWaitEvent(s, a->join, 0);
+    }
+  }
+};
+
 int launch_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_t num_experts,
                           int32_t* counts, int32_t* offsets, int32_t* block_base,
                           int32_t* mtile_offsets, int32_t* mtile_list, float* amax_reset,
@@ -729,16 +750,17 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
   if (aux) {
     // fork: both GEMMs of the narrow experts on the auxiliary stream, enqueued
     // first so that their workgroups find free CUs; join before the combine
-    const int ncus = std::min(nc.cus, device_cus());
+    const int ncus = narrow_cus_limit(nc.cus);
     // Which workgroups work is decided on the device from narrow_info: with
     // experts of both kinds the narrow kernels use ncus workgroups and (share)
     // the first 256x256 GEMM leaves them those CUs; with one kind only, that
     // kind gets every CU it was launched on.
     if (hipEventRecord(aux->fork, s) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: fork event failed");
-    const int yield_from = nc.share ? std::max(1, device_cus() - ncus) : 0;
+    const int yield_from = nc.share ? device_cus() - ncus : 0;  // >= device_cus() / 4
     if (hipStreamWaitEvent(aux->aux, aux->fork, 0) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: fork to the auxiliary stream failed");
+    AuxJoin guard{aux, s};
     // the narrow kernels launch one workgroup per CU: beside 256x256 tiles the
     // first ncus to start take items, else all of them (decode-like shapes)
     const int ngrid = device_cus();
@@ -773,6 +795,7 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
                               stream, w.narrow_info, 0, 0));
     if (!late_join && hipStreamWaitEvent(s, aux->join, 0) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: join of the auxiliary stream failed");
+    guard.armed = false;  // joined above
     aux_lock.unlock();
     HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
     return HKMOE_OK;

@@ -27,12 +27,13 @@
 //    free whether the LDS serves 8 or 16 lanes per cycle, and the XOR is a lane
 //    constant for every fragment; the swizzle is applied on the global side
 //    because the DMA writes lanes linearly.
-//  * 128x128 weight / 1x128 activation block scales: K step == scale block, so
-//    the accumulator is kept in units of the current block's scale product,
-//        u_k = u_{k-1} * (s_{k-1} / s_k) + P_k,   C = u_last * s_last,
-//    i.e. one multiply of the accumulator before the block's MFMA (no
-//    MFMA -> VALU dependency, no partial-sum registers).  Scales must be
-//    positive normal fp32 numbers (the quantisers floor them at 2^-126).
+//  * 128x128 weight / 1x128 activation block scales: K step == scale block ==
+//    the K extent of one v_mfma_f32_16x16x128, so every MFMA of a step starts
+//    from zero and yields the block's raw product P_k, which is folded in as
+//        C = fma(P_k, s_a[row, k] * s_w[col block, k], C)
+//    (4 FMAs per MFMA, issued under the next MFMA).  C is in true units at
+//    every step: no division by a scale, so no overflow when a block's scale
+//    is tiny next to the previous one's, and no final rescale.
 //  * MX (OCP microscaling) mode: 1x32 e8m0 exponents per row of A and of B,
 //    applied inside the MFMA (v_mfma_scale_f32_16x16x128_f8f6f4), which takes
 //    the exponent of row l%16 and K block l/16 from lane l: one e8m0 byte per
@@ -205,6 +206,16 @@ __device__ __forceinline__ void mx_subtile(f32x4 (&acc)[4], const i32x8 (&bf)[4]
   acc[1] = mfma_mx<1, U>(bf[1], af, acc[1], sb, sa);
   acc[2] = mfma_mx<2, U>(bf[2], af, acc[2], sb, sa);
   acc[3] = mfma_mx<3, U>(bf[3], af, acc[3], sb, sa);
+}
+
+// Block scales: c += f * p element-wise, one fused multiply-add each (p: one
+// K block's raw MFMA product, f: its scale product).  The 256x256 and the
+// narrow kernel both fold through here, so they give the same bits.
+__device__ __forceinline__ void fold_block(f32x4& c, const f32x4& p, float f) {
+  c[0] = __builtin_fmaf(p[0], f, c[0]);
+  c[1] = __builtin_fmaf(p[1], f, c[1]);
+  c[2] = __builtin_fmaf(p[2], f, c[2]);
+  c[3] = __builtin_fmaf(p[3], f, c[3]);
 }
 
 // Wait for this wave's outstanding DMA and LDS reads, then the workgroup
@@ -486,14 +497,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     wait_dma(k_steps > 1);     // stage 0 (and the weight scales) visible to all
     if (grp == 1) sync_lds();  // group 1 runs one phase behind group 0
 
-    // block scales: the accumulator holds sum / (sa_prev[i] * sb_prev[h]).
-    // The previous scales start at 0, so the first step's factor is exactly 0
-    // (the accumulators are 0 then): no first-step special case.
-    float sa_prev[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sa_prev[i] = 0.0f;
-    float sb_prev0 = 0.0f, sb_prev1 = 0.0f;
-    float sa_cur[8], sb_cur0 = 1.0f, sb_cur1 = 1.0f, rb0 = 0.0f, rb1 = 0.0f;
+    // block scales of the current K step: the activation scale of each of the
+    // lane's 8 sub-tile rows, and the weight scale of its gate / up (or only)
+    // 128-column block
+    float sa_cur[8], sb_cur0 = 1.0f, sb_cur1 = 1.0f;
 
     // Four barrier-separated phases per K step: memory (LDS fragment reads,
     // DMA issue), compute (MFMAs from registers only), memory, compute.  Group
@@ -554,27 +561,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       __builtin_amdgcn_sched_barrier(0);
 
       // ---- compute phase 1: sub-tiles 0-3
-      // Block scales: factors r = (s_prev / s_cur) per sub-tile row and column
-      // half, applied to each accumulator right before its MFMA, so the
-      // multiplies of one accumulator overlap the MFMA of the previous one.
       auto compute = [&](int i0) {
         __builtin_amdgcn_s_setprio(1);
-        float r0[4], r1[4];
-        if constexpr (kBlockSc) {
-          if (i0 == 0) {
-            rb0 = sb_prev0 * __builtin_amdgcn_rcpf(sb_cur0);
-            rb1 = sb_prev1 * __builtin_amdgcn_rcpf(sb_cur1);
-            sb_prev0 = sb_cur0;
-            sb_prev1 = sb_cur1;
-          }
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float ra = sa_prev[i0 + u] * __builtin_amdgcn_rcpf(sa_cur[i0 + u]);
-            r0[u] = ra * rb0;
-            r1[u] = ra * rb1;
-            sa_prev[i0 + u] = sa_cur[i0 + u];
-          }
-        }
         // Skipped only when all four sub-tiles are dead; a partly live phase
         // also computes its dead sub-tiles (stale fragments, never stored).
         if (live_sub > i0) {
@@ -584,11 +572,30 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
             mx_subtile<1>(acc[i0 + 1], bf, af[1], mx_sb, sa_w);
             mx_subtile<2>(acc[i0 + 2], bf, af[2], mx_sb, sa_w);
             mx_subtile<3>(acc[i0 + 3], bf, af[3], mx_sb, sa_w);
+          } else if constexpr (kBlockSc) {
+            // factor of sub-tile u: its row's activation scale times the
+            // weight scale of the column block (gate: j < 2, up: j >= 2)
+            float f0[4], f1[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              f0[u] = sa_cur[i0 + u] * sb_cur0;
+              f1[u] = kSilu ? sa_cur[i0 + u] * sb_cur1 : f0[u];
+            }
+            // MFMA t from zero; the FMAs of MFMA t-1 follow it, so they run
+            // while MFMA t occupies the matrix core
+            f32x4 prev = mfma_e4m3_16x16x128(bf[0], af[0], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int t = 1; t <= 16; ++t) {
+              f32x4 cur;
+              if (t < 16) cur = mfma_e4m3_16x16x128(bf[t & 3], af[t >> 2], f32x4{0.f, 0.f, 0.f, 0.f});
+              const int u = (t - 1) >> 2, j = (t - 1) & 3;
+              fold_block(acc[i0 + u][j], prev, (kSilu && j >= 2) ? f1[u] : f0[u]);
+              if (t < 16) prev = cur;
+            }
           } else {
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
               const int u = t >> 2, j = t & 3;
-              if constexpr (kBlockSc) acc[i0 + u][j] *= (kSilu && j >= 2) ? r1[u] : r0[u];
               acc[i0 + u][j] = mfma_e4m3_16x16x128(bf[j], af[u], acc[i0 + u][j]);
             }
           }
@@ -621,13 +628,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     // ---- epilogue ----------------------------------------------------------
     // lane holds, for sub-tile i and n fragment j, output row wave_row0+16i+l16
     // and columns 16*j + 4*lg .. +3 of the wave's 64-column quarter
+    // per-tensor scales are applied here; block-scaled and MX accumulators
+    // already hold the scaled sums
     float tens = 1.0f;
     if constexpr (SC == Scale::kTensor)
       tens = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
-    auto fac = [&](int i, int h) -> float {
-      if constexpr (kBlockSc) return sa_prev[i] * (h ? sb_prev1 : sb_prev0);
-      else return tens;
-    };
+    auto fac = [&](int, int) -> float { return tens; };
 
     if constexpr (EPI == Epi::kStoreF32) {
 #pragma unroll

@@ -23,7 +23,7 @@
 //      plain GEMM:   rows 32w..32w+31 of the 256.
 //    Each lane loads its fragment rows' 32 K bytes per step with two 16-byte
 //    buffer loads per fragment, in the register order read_frag produces from
-//    LDS: the MFMA operands, the rescale arithmetic and the epilogue are those
+//    LDS: the MFMA operands, the block-scale arithmetic and the epilogue are those
 //    of the 256x256 kernel, so both kernels give the same bits.
 //  * activations: every wave DMAs 8 of the segment's 64 rows (rows past the
 //    segment repeat its last row) into an LDS ring of P+1 stages, loaded P
@@ -386,9 +386,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
       acc[i][0] = f32x4{0.f, 0.f, 0.f, 0.f};
       acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    float sa_prev[MF] = {0.f, 0.f, 0.f, 0.f};
-    float sb_prev0 = 0.f, sb_prev1 = 0.f;
-
     for (int g = 0; g < groups; ++g) {
       const bool last_group = (g == groups - 1);
       if (g == dgroup && tid == 0) lds_write_i32(q_addr, nxt);  // read after the barrier below
@@ -424,24 +421,25 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
         const float2 sbv = lds_read_w2(sbuf + sb_wave + kt * 4);
         const float sb_cur0 = sbv.x;                   // lane 0's DMA: gate / only block
         const float sb_cur1 = kSilu ? sbv.y : sbv.x;   // lane 1's DMA: up block
-        // rescale and MFMAs, in the 256x256 kernel's arithmetic
-        const float rb0 = sb_prev0 * __builtin_amdgcn_rcpf(sb_cur0);
-        const float rb1 = sb_prev1 * __builtin_amdgcn_rcpf(sb_cur1);
-        sb_prev0 = sb_cur0;
-        sb_prev1 = sb_cur1;
+        // MFMAs from zero folded in with the block's scale product, in the
+        // 256x256 kernel's arithmetic (fold_block)
         // fragment i (rows 16i..16i+15) only while the segment reaches it
         auto frag_step = [&](auto i_tag) {
           constexpr int i = decltype(i_tag)::value;
           i32x8 af;
           float sa_cur;
           lds_frag<2048 * i, 64 * i>(st + lo_off, st + hi_off, sa_addr, af, sa_cur);
-          const float ra = sa_prev[i] * __builtin_amdgcn_rcpf(sa_cur);
-          const float r0 = ra * rb0, r1 = ra * rb1;
-          sa_prev[i] = sa_cur;
-          acc[i][0] *= r0;
-          acc[i][0] = mfma_e4m3_16x16x128(wbuf[s][0], af, acc[i][0]);
-          acc[i][1] *= kSilu ? r1 : r0;
-          acc[i][1] = mfma_e4m3_16x16x128(wbuf[s][1], af, acc[i][1]);
+          const float f0 = sa_cur * sb_cur0;
+          const float f1 = kSilu ? sa_cur * sb_cur1 : f0;
+          const f32x4 p0 = mfma_e4m3_16x16x128(wbuf[s][0], af, f32x4{0.f, 0.f, 0.f, 0.f});
+          const f32x4 p1 = mfma_e4m3_16x16x128(wbuf[s][1], af, f32x4{0.f, 0.f, 0.f, 0.f});
+          fold_block(acc[i][0], p0, f0);
+          fold_block(acc[i][1], p1, f1);
+          // each fragment's products are folded before the next fragment's LDS
+          // reads (an empty volatile asm that takes the accumulators): the
+          // kernel's VGPRs hold the weight prefetch window, and MFMA
+          // temporaries sunk past the next fragments would spill it
+          asm volatile("" : "+v"(acc[i][0]), "+v"(acc[i][1]));
         };
         frag_step(std::integral_constant<int, 0>{});
         if (mf > 1) frag_step(std::integral_constant<int, 1>{});
@@ -459,20 +457,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
     }
 
     // ---- epilogue (the next item's first P steps are in flight) ----------
-    auto fac = [&](int i, int h) -> float { return sa_prev[i] * (h ? sb_prev1 : sb_prev0); };
+    // the accumulators hold the block-scaled sums
     if constexpr (!kSilu) {
 #pragma unroll
       for (int i = 0; i < MF; ++i) {
         const int r = 16 * i + l16;
         if (i < mf && r < C.valid) {
-          const float f = fac(i, 0);
           uint16_t* yrow = static_cast<uint16_t*>(p.c) + static_cast<int64_t>(C.row0 + r) * p.n_out +
                            C.nt * kBN + 32 * wave + 4 * lg;
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             uint2 v;
-            v.x = pack_bf16x2(acc[i][j][0] * f, acc[i][j][1] * f);
-            v.y = pack_bf16x2(acc[i][j][2] * f, acc[i][j][3] * f);
+            v.x = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+            v.y = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
             *reinterpret_cast<uint2*>(yrow + 16 * j) = v;
           }
         }
@@ -483,10 +480,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < MF; ++i) {
         if (i >= mf) break;
-        const float fg = fac(i, 0), fu = fac(i, 1);
         float hv[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) hv[q] = silu(acc[i][0][q] * fg) * (acc[i][1][q] * fu);
+        for (int q = 0; q < 4; ++q) hv[q] = silu(acc[i][0][q]) * acc[i][1][q];
         uint2 v;
         v.x = pack_bf16x2(hv[0], hv[1]);
         v.y = pack_bf16x2(hv[2], hv[3]);

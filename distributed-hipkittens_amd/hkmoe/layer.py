@@ -192,11 +192,14 @@ def moe_forward_steps(x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, to
     return r
 
 
-def narrow_grid(rows, num_experts, cus, max_rows, n_cu):
-    """Workgroups of the narrow kernels, as hkmoe_moe_forward chooses them: one
-    per CU when the average expert fits the narrow kernel (decode-like shapes,
-    where most experts are narrow), else ``cus``."""
-    return n_cu if rows <= num_experts * max_rows else cus
+def narrow_cus(cus, n_cu):
+    """Workgroups the narrow kernels take while 256x256 tiles exist, as
+    hkmoe_moe_forward limits them: at most three quarters of the CUs.  Both
+    narrow kernels launch one workgroup per CU and the device lifts the limit
+    when every expert is narrow, so passing this as ``grid`` of the part-1
+    dispatches gives hkmoe_moe_forward's schedule; the first 256x256 GEMM then
+    runs on ``n_cu - cus`` workgroups (wide_share >= 1)."""
+    return min(cus, n_cu - n_cu // 4)
 
 
 def _steps_narrow(r, x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top_k, packed, narrow):
@@ -215,15 +218,15 @@ def _steps_narrow(r, x_q, x_scale, logits, w13_q, w13_scale, w2_q, w2_scale, top
     side.wait_stream(main)
     split = dict(packed=packed, mtile_list=r["mtile_list"], narrow_info=r["narrow_info"])
     n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
-    grid = narrow_grid(t * top_k, w13_q.shape[0], cus, max_rows, n_cu)
+    cus = narrow_cus(cus, n_cu)
     with torch.cuda.stream(side):
         tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale, r["offsets"],
-                                         r["mtile_offsets"], r["hq"], r["hs"], None, part=1, grid=grid, **split)
+                                         r["mtile_offsets"], r["hq"], r["hs"], None, part=1, grid=cus, **split)
         tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2_q, w2_scale, r["offsets"], r["mtile_offsets"],
-                                         r["y"], None, part=1, grid=grid, **split)
+                                         r["y"], None, part=1, grid=cus, **split)
     tk_kernel.dispatch_grouped_gemm1(x_q, x_scale, r["perm"], top_k, w13_q, w13_scale, r["offsets"],
                                      r["mtile_offsets"], r["hq"], r["hs"], r["tile_ctr"][:8], part=0,
-                                     grid=max(1, n_cu - cus) if share else 0, **split)
+                                     grid=n_cu - cus if share else 0, **split)
     tk_kernel.dispatch_grouped_gemm2(r["hq"], r["hs"], w2_q, w2_scale, r["offsets"], r["mtile_offsets"],
                                      r["y"], r["tile_ctr"][8:], part=0, grid=0, **split)
     main.wait_stream(side)

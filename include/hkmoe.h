@@ -251,7 +251,9 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
  * (both GEMMs) that runs on `cus` workgroups on a library-owned auxiliary
  * stream, beside the 256x256 kernels of the larger experts on the caller's
  * stream; the caller's stream waits for it before the combine.  Results are
- * bit-identical with the narrow path on or off.  cus == 0 turns it off;
+ * bit-identical with the narrow path on or off.  cus == 0 turns it off; while
+ * 256x256 tiles exist the narrow kernels take at most three quarters of the
+ * device's CUs, whatever cus asks for (the first wide GEMM keeps the rest);
  * wide_share 1 or 2 runs the first wide GEMM on (CUs - cus) workgroups while
  * narrow experts exist; with 2 the narrow path's CUs also join that GEMM's
  * remaining tiles once both narrow GEMMs are done (a second launch of it on the

@@ -10,6 +10,11 @@ Bar: every replay equals the eager call on the same inputs, bit for bit.  Each
 input set is replayed twice; between replays the test runs other eager work
 (copies, and an eager call of the same layer object, on the same workspace, on
 other inputs) and synchronises, and that eager result is checked as well.
+
+The narrow path (block scales, even H/128 and I/128) forks to the library's
+auxiliary stream and joins back through events; under capture the auxiliary
+stream joins the graph the same way, with the late join (wide_share 2) and
+without it (1).
 """
 import pytest
 import torch
@@ -102,3 +107,33 @@ def test_moe_layer_mx_graph_replay(hk):
         x_q, x_e = hk.quant_mx(torch.randn((T, H), generator=gen, device="cuda"))
         sets.append((x_q, x_e, _logits(gen)))
     _replay_and_check(layer, sets)
+
+
+@pytest.mark.parametrize("share", [1, 2])
+def test_moe_layer_graph_replay_narrow(hk, share):
+    """Block-scaled layer with experts of both kinds (<= 32 rows: narrow kernel;
+    larger: 256x256) captured with the narrow path on."""
+    t, h, i, e, k = 300, 512, 256, 32, 4
+    saved = hk.tk_kernel.get_narrow()
+    # T*k = 1200 > E*32: the late join runs with share 2
+    hk.tk_kernel.set_narrow(16, 32, share)
+    try:
+        gen = torch.Generator(device="cuda").manual_seed(77 + share)
+        w13_q, w13_s = hk.quant_block(torch.randn((e, 2 * i, h), generator=gen, device="cuda"))
+        w2_q, w2_s = hk.quant_block(torch.randn((e, h, i), generator=gen, device="cuda"))
+        layer = hk.MoELayer(w13_q, w13_s, w2_q, w2_s, k)
+        sets = []
+        for _ in range(N_SETS):
+            x_q, x_s = hk.quant_group(torch.randn((t, h), generator=gen, device="cuda"))
+            lg = torch.randn((t, e), generator=gen, device="cuda")
+            rank = torch.randperm(e, generator=gen, device="cuda").float() + 1.0
+            lg = lg - 1.1 * torch.log(rank)[None, :]
+            sets.append((x_q, x_s, lg))
+            r = hk.moe_forward_steps(x_q, x_s, lg, layer.w13_q, w13_s, layer.w2_q, w2_s, k, packed=True,
+                                     narrow=(16, 32, share))
+            torch.cuda.synchronize()
+            counts = r["counts"].cpu()
+            assert int(r["narrow_info"][0]) > 0 and (counts > 32).any()
+        _replay_and_check(layer, sets)
+    finally:
+        hk.tk_kernel.set_narrow(*saved)

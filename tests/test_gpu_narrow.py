@@ -1,7 +1,7 @@
 """Narrow path of the one-call layer (experts of <= 64 rows in the
 weight-streaming kernel on an auxiliary stream) against the 256x256 kernels.
 
-The narrow kernel uses the 256x256 kernel's operand order, rescale arithmetic
+The narrow kernel uses the 256x256 kernel's operand order, block-scale arithmetic
 and epilogue, so the layer output is bit-identical with the narrow path off,
 on, on a tiny grid (many items per workgroup), with a lower row threshold, and
 with the narrow path's CUs joining the first 256x256 GEMM's tiles afterwards
@@ -79,8 +79,10 @@ def test_narrow_bit_exact(hk, narrow_restore, name, packed):
     # threshold 16 with wide_share 2: where T*k > 16*E (p8_g2_g1, p4_p2, dsv3_shape)
     # the narrow CUs also join the first 256x256 GEMM's tiles (late join)
     print(f"  experts of 1..16 rows: {int(((counts > 0) & (counts <= 16)).sum())}", flush=True)
+    # (4096, 64, 1): more CUs than the device has; the library keeps a quarter
+    # of them for the first 256x256 GEMM
     for cus, max_rows, share in ((48, 64, 0), (3, 64, 0), (48, 16, 0), (40, 64, 1), (64, 64, 2), (3, 64, 1),
-                                 (64, 16, 2), (3, 16, 2)):
+                                 (64, 16, 2), (3, 16, 2), (4096, 64, 1)):
         hk.tk_kernel.set_narrow(cus, max_rows, share)
         on = _one_call(hk, g, w13, w2, packed)
         assert torch.equal(on.view(torch.int16), off.view(torch.int16)), (cus, max_rows, share)
