@@ -196,6 +196,37 @@ int get_aux(hipStream_t main_stream, AuxStreams** out) {
   return HKMOE_OK;
 }
 
+// The allocation-free layer's workspace: one array per device, created with
+// the code object, held until the process ends.  In host code `scratch` names
+// a host-side stand-in: its device address (different on every GPU) comes from
+// hipGetSymbolAddress, looked up once per device on the first call with that
+// device current, and only that address is passed to kernels.
+constexpr size_t kScratchBytes = HKMOE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_ptr(void** out) {
+  *out = nullptr;
+  int dev = 0;
+  const hipError_t gerr = hipGetDevice(&dev);
+  if (gerr != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(HKMOE_ERR_HIP, "moe_forward_noalloc: no usable current device (%s)", hipGetErrorString(gerr));
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return fail(HKMOE_ERR_HIP, "moe_forward_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(err));
+    if ((reinterpret_cast<uintptr_t>(p) & 255) != 0)
+      return fail(HKMOE_ERR_HIP, "moe_forward_noalloc: scratch of device %d is not 256-byte aligned", dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HKMOE_OK;
+}
+
 // Workgroups the narrow kernels may take while 256x256 tiles exist: at most
 // three quarters of the CUs, so the first 256x256 GEMM keeps at least a quarter
 // of them whatever hkmoe_set_narrow asked for.
@@ -701,11 +732,13 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
   return carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, scale_mode).bytes;
 }
 
-int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
-                      const float* w13_scale, const void* w2, const float* w2_scale,
-                      int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
-                      int32_t inter, int scale_mode, int w_layout, void* out, void* workspace,
-                      size_t workspace_bytes, hkmoe_stream_t stream) {
+// The layer; aux_ok: the narrow path may fork to the library's auxiliary
+// stream (else every kernel runs on `stream`, with the narrow path off).
+static int moe_forward_impl(const void* x_q, const float* x_scale, const float* logits, const void* w13,
+                            const float* w13_scale, const void* w2, const float* w2_scale,
+                            int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
+                            int32_t inter, int scale_mode, int w_layout, void* out, void* workspace,
+                            size_t workspace_bytes, hkmoe_stream_t stream, bool aux_ok) {
   HK_REQUIRE(x_q && x_scale && logits && w13 && w13_scale && w2 && w2_scale && out,
              "moe_forward: null pointer");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
@@ -735,7 +768,7 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
   // beside the 256x256 kernels of the larger experts on the main stream.
   const NarrowConfig nc = narrow_config();
   AuxStreams* aux = nullptr;
-  if (block && nc.cus > 0 && nc.max_rows > 0 && narrow_depth(hidden / kBK) > 0 &&
+  if (aux_ok && block && nc.cus > 0 && nc.max_rows > 0 && narrow_depth(hidden / kBK) > 0 &&
       narrow_depth(inter / kBK) > 0)
     HK_TRY(get_aux(s, &aux));
   std::unique_lock<std::mutex> aux_lock(g_aux_mu, std::defer_lock);
@@ -817,6 +850,15 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
                              w.tile_ctr + 8, stream));
   HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
   return HKMOE_OK;
+}
+
+int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
+                      const float* w13_scale, const void* w2, const float* w2_scale,
+                      int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
+                      int32_t inter, int scale_mode, int w_layout, void* out, void* workspace,
+                      size_t workspace_bytes, hkmoe_stream_t stream) {
+  return moe_forward_impl(x_q, x_scale, logits, w13, w13_scale, w2, w2_scale, num_tokens, num_experts, top_k,
+                          hidden, inter, scale_mode, w_layout, out, workspace, workspace_bytes, stream, true);
 }
 
 // ---------------------------------------------------------------------------
@@ -1098,5 +1140,31 @@ int hkmoe_moe_forward_mx(const void* x_q, const void* x_e8m0, const float* logit
                                 num_experts, hidden, inter, w_layout, w.y, w.tile_ctr + 8, stream));
   HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
   return HKMOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// allocation-free layer (hkmoe_moe_forward_noalloc)
+// ---------------------------------------------------------------------------
+int hkmoe_moe_forward_noalloc(const void* x_q, const float* x_scale, const float* logits, const void* w13,
+                              const float* w13_scale, const void* w2, const float* w2_scale,
+                              int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
+                              int32_t inter, int scale_mode, int w_layout, void* out, hkmoe_stream_t stream) {
+  HK_REQUIRE(num_tokens >= 0 && num_experts >= 1 && top_k >= 1 && hidden > 0 && inter > 0,
+             "moe_forward_noalloc: bad shape");
+  HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
+             "moe_forward_noalloc: bad scale_mode %d", scale_mode);
+  const size_t need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, scale_mode).bytes;
+  if (need > kScratchBytes)
+    return fail(HKMOE_ERR_WORKSPACE,
+                "moe_forward_noalloc: the layer needs %zu bytes of workspace, the library's per-device scratch "
+                "holds %zu (HKMOE_NOALLOC_SCRATCH_BYTES); pass a workspace to hkmoe_moe_forward instead",
+                need, kScratchBytes);
+  if (num_tokens == 0) return moe_forward_impl(x_q, x_scale, logits, w13, w13_scale, w2, w2_scale, num_tokens,
+                                               num_experts, top_k, hidden, inter, scale_mode, w_layout, out,
+                                               nullptr, 0, stream, false);
+  void* ws = nullptr;
+  HK_TRY(scratch_ptr(&ws));
+  return moe_forward_impl(x_q, x_scale, logits, w13, w13_scale, w2, w2_scale, num_tokens, num_experts, top_k,
+                          hidden, inter, scale_mode, w_layout, out, ws, kScratchBytes, stream, false);
 }
 }  // extern "C"

@@ -276,6 +276,32 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
                       size_t workspace_bytes, hkmoe_stream_t stream);
 
 /*
+ * hkmoe_moe_forward without a workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  No counterpart in the reference.
+ *
+ * Same arguments, results and errors as hkmoe_moe_forward (bit for bit), and it
+ * allocates nothing: the layer's workspace is the library's per-device scratch
+ * array of HKMOE_NOALLOC_SCRATCH_BYTES (64 MiB), which every GPU the library
+ * runs on holds until the process ends.  A layer whose workspace
+ * (hkmoe_moe_workspace_size) is larger is rejected with HKMOE_ERR_WORKSPACE
+ * before any launch.  Largest T that fits: 509 for config-3 shapes (H=7168,
+ * I=2048, E=256, top-8, block scales), 856 for config-5 shapes (H=4096, I=1536,
+ * E=128, top-8), 655 for config-2 shapes (H=4096, I=14336, E=8, top-2,
+ * per-tensor scales).  Every kernel runs on `stream` (the narrow path's auxiliary stream is
+ * not used).  The first call on a device looks up that device's scratch
+ * address (hipGetSymbolAddress): make it outside graph capture.  All calls on
+ * one device share its scratch and each call leaves its intermediates there:
+ * calls that overlap in time on one device (other streams, other threads)
+ * race and must be serialised by the caller.
+ */
+#define HKMOE_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int hkmoe_moe_forward_noalloc(const void* x_q, const float* x_scale, const float* logits, const void* w13,
+                              const float* w13_scale, const void* w2, const float* w2_scale,
+                              int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
+                              int32_t inter, int scale_mode, int w_layout, void* out, hkmoe_stream_t stream);
+
+/*
  * Synthetic-input helpers (quantisers): x [R, C] fp32 on the device.
  *   hkmoe_quant_group:  q [R,C] e4m3, s [R, C/128]  (1x128 groups, row-major s)
  *   hkmoe_quant_block:  q [B,R,C] e4m3, s [B, R/128, C/128] (128x128 blocks)
