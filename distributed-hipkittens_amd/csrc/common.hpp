@@ -182,4 +182,13 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
+// The lane id computed where it is used (a volatile asm is neither hoisted nor
+// shared): for code that runs once per tile in a kernel at the VGPR limit,
+// where a lane constant hoisted to the kernel entry would be spilled.
+__device__ __forceinline__ int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 }  // namespace hkmoe

@@ -71,6 +71,8 @@
 //    requantisation to e4m3 + scales (block mode).
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace hkmoe {
@@ -124,19 +126,27 @@ struct GemmParams {
 constexpr int kBM = 256, kBN = 256, kBK = 128;
 constexpr int kThreads = 512;
 constexpr int kTileBytes = kBM * kBK;                    // 32 KiB per operand per stage
-constexpr int kScaleBytes = kBM * 4;                     // activation scales of one K block
+constexpr int kScaleBytes = kBM * 4;                     // activation scales (or MX words) of one K block
 constexpr int kStageBytes = 2 * kTileBytes + kScaleBytes;
 constexpr int kMaxKBlocks = 128;                         // K <= 16384
-constexpr int kBsBytes = 2 * kMaxKBlocks * 4;            // weight scales of one tile
-constexpr int kMainLds = 2 * kStageBytes + kBsBytes;
-// epilogue staging of a bf16 output tile, rows padded by 16 bytes
-constexpr int kCtLdStore = kBN + 8;                      // bf16 elements per staged row
-constexpr int kCtLdSilu = 128 + 8;
-constexpr int kEpiLds = kBM * kCtLdStore * 2;
-static_assert(kBM * kCtLdSilu * 2 + kBM * 4 <= kEpiLds, "SiLU staging + MX exponents fit the epilogue LDS");
-constexpr int kLdsData = kMainLds > kEpiLds ? kMainLds : kEpiLds;
-constexpr int kLdsBytes = kLdsData + 16;                 // + the broadcast slot of the tile queue
-constexpr int kGroupM = 8;
+// LDS: two operand stages (in MX mode each 1 KiB larger, for the B exponent
+// words), then
+//   weight scales of two tiles (current / next)  [2][2 column blocks][kMaxKBlocks] fp32
+//   gathered A rows of the next tile             [256] int32
+//   epilogue scratch                             row maxima [256][4] fp32, or MX exponents
+//   tile slots                                   [0, 1] first tile (m, n); [2..7] next tile
+//                                                (m, n, expert, first row, rows, MX M tile)
+// The epilogue stages its output tile in the A half of the last K step's
+// stage (nothing else is live there) and this scratch, so the next tile's
+// first stages can be in flight while it runs.
+constexpr int kStageMax = kStageBytes + kScaleBytes;
+// K-step variants of the persistent kernel: which next-tile work a step carries
+constexpr int kPlain = 0, kClaim = 1, kLookup = 2, kPublish = 3, kStage = 4, kNextB0 = 5, kNextA0 = 6;
+constexpr int kBsOff = 2 * kStageMax;
+constexpr int kRowsOff = kBsOff + 2 * 2 * kMaxKBlocks * 4;
+constexpr int kEpiOff = kRowsOff + kBM * 4;
+constexpr int kSlotOff = kEpiOff + kBM * 4 * 4;
+constexpr int kLdsBytes = kSlotOff + 32;
 
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 
@@ -228,10 +238,32 @@ __device__ __forceinline__ void sync_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// B source of the tile (expert e, N tile nt) for one wave: buffer descriptor,
+// lane offset within a K step, and the K-step stride (see the B layout notes
+// in gemm_fp8_persistent).  A plain function with scalar parameters: in a
+// lambda the same code made the compiler keep lane constants in private memory.
+__device__ __forceinline__ void b_source(const GemmParams& p, int e, int nt, bool silu, int wg, i32x4& srd,
+                                         int& voff, int& kstride) {
+  const int lane = lane_here();
+  if (p.b_packed) {
+    srd = make_srd(p.b + (static_cast<int64_t>(e) * (p.nb / kBN) + nt) * kBN * p.K,
+                   static_cast<uint32_t>(kBN) * p.K);
+    voff = wg * 8 * kBK + lane * 16;
+    kstride = kTileBytes;
+  } else {
+    srd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K, static_cast<uint32_t>(p.nb) * p.K);
+    const int ld_row = 8 * wg + (lane >> 3), ld_chunk = (lane & 7) ^ swz(ld_row);
+    const int b_row0 = silu ? nt * 128 + ld_row : nt * kBN + ld_row;
+    voff = b_row0 * p.K + ld_chunk * 16;
+    kstride = kBK;
+  }
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wunused-lambda-capture"
 template <Epi EPI, Scale SC>
 __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  float* bs_lds = reinterpret_cast<float*>(smem + 2 * kStageBytes);  // [2][k_blocks]
 
   constexpr bool kBlockSc = (SC == Scale::kBlock);
   constexpr bool kMX = (SC == Scale::kMX);
@@ -239,7 +271,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   // stage: A tile, B tile, A scales (1 KiB) and, in MX mode, B scales (1 KiB)
   constexpr int kStg = kMX ? kStageBytes + kScaleBytes : kStageBytes;
   static_assert(EPI != Epi::kSiluMx || kMX, "MX requantisation needs MX scales");
-  static_assert(2 * kStg <= kLdsData, "LDS budget");
+  static_assert(2 * kStg <= kBsOff, "LDS budget");
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -279,198 +311,285 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   const int bm = 1 << p.blk_m_log2, bn = 32 >> p.blk_m_log2;
   const int nbn = (p.n_tiles + bn - 1) / bn;
   const int nblocks = ((total_mtiles + bm - 1) / bm) * nbn;
-  int* s_tile = reinterpret_cast<int*>(smem + kLdsData);
+#define HK_SLOT reinterpret_cast<int*>(smem + kSlotOff)
+#define HK_NROW reinterpret_cast<int*>(smem + kRowsOff)
+#define HK_BS reinterpret_cast<float*>(smem + kBsOff)
   const int xcd = blockIdx.x & 7;
-  int steal = 0;          // queues visited so far (thread 0 only)
-  int static_j = vid;     // static schedule: next slot index
+#define HK_CAP tid, wave, lane, grp, wg, l16, lg, wave_row0, fx, dense, total_mtiles, k_steps, ld_row, ld_chunk, xcd
+  int steal = 0;       // thread 0: tile queues visited so far
+  int static_j = vid;  // thread 0: the static schedule's next slot
 
-  while (true) {
-    // ---- next tile: slot j of queue q -> block b = q + 8*(j/32) -----------
-    int mt_glob = -1, nt = 0;
-    if (p.tile_ctr != nullptr) {
-      if (tid == 0) {
-        int t = -1;
-        while (steal < 8 && t < 0) {
-          const int q = (xcd + steal) & 7;
-          const int nslots = q < nblocks ? 32 * ((nblocks - q + 7) >> 3) : 0;
-          const int j = nslots > 0 ? atomicAdd(&p.tile_ctr[q], 1) : nslots;
-          if (j >= nslots) { ++steal; continue; }
-          const int b = q + 8 * (j >> 5), sl = j & 31;
-          const int m = bm * (b / nbn) + (sl & (bm - 1)), n = bn * (b % nbn) + (sl >> p.blk_m_log2);
-          if (m < total_mtiles && n < p.n_tiles) t = m * p.n_tiles + n;
-        }
-        *s_tile = t;
-      }
-      __syncthreads();
-      const int t = *s_tile;
-      if (t < 0) break;
-      mt_glob = t / p.n_tiles;
-      nt = t - mt_glob * p.n_tiles;
-    } else {
-      // same blocks, walked statically: vid-th slot of every round of g slots
-      bool found = false;
-      while (!found) {
-        const int j = static_j;
+  // ---- tile source (thread 0) ------------------------------------------------
+  // With tile counters, slot j of queue q is tile (m, n) of block b = q + 8*(j/32);
+  // a drained queue moves on to the next XCD's.  Without, the same blocks are
+  // walked statically: the vid-th slot of every round of g slots.  A claim is
+  // split in two: claim_start issues the atomic on the current queue and
+  // claim_end, which may run a K step later, turns its slot into a tile (or
+  // takes further slots: past a queue's end, or outside the tile grid).
+  auto tile_of = [&, HK_CAP](int b, int sl, int& n) __attribute__((always_inline)) -> int {
+    const int m = bm * (b / nbn) + (sl & (bm - 1));
+    n = bn * (b % nbn) + (sl >> p.blk_m_log2);
+    return (m < total_mtiles && n < p.n_tiles) ? m : -1;
+  };
+  auto queue_slots = [&, HK_CAP](int q) __attribute__((always_inline)) -> int {
+    return q < nblocks ? 32 * ((nblocks - q + 7) >> 3) : 0;
+  };
+  auto claim_start = [&, HK_CAP]() __attribute__((always_inline)) -> int {
+    if (p.tile_ctr == nullptr || steal >= 8) return 0;
+    const int q = (xcd + steal) & 7;
+    return queue_slots(q) > 0 ? atomicAdd(&p.tile_ctr[q], 1) : 0;
+  };
+  auto claim_end = [&, HK_CAP](int j, int& n) __attribute__((always_inline)) -> int {  // m, or -1
+    if (p.tile_ctr == nullptr) {
+      while (true) {
+        const int js = static_j;
         static_j += g;
-        const int b = j >> 5, sl = j & 31;
-        if (b >= nblocks) break;
-        const int m = bm * (b / nbn) + (sl & (bm - 1)), n = bn * (b % nbn) + (sl >> p.blk_m_log2);
-        if (m < total_mtiles && n < p.n_tiles) { mt_glob = m; nt = n; found = true; }
+        if ((js >> 5) >= nblocks) return -1;
+        const int m = tile_of(js >> 5, js & 31, n);
+        if (m >= 0) return m;
       }
-      if (!found) break;
     }
-    mt_glob = __builtin_amdgcn_readfirstlane(mt_glob);
-    nt = __builtin_amdgcn_readfirstlane(nt);
+    while (steal < 8) {
+      const int q = (xcd + steal) & 7;
+      if (j < queue_slots(q)) {
+        const int m = tile_of(q + 8 * (j >> 5), j & 31, n);
+        if (m >= 0) return m;
+      } else {
+        ++steal;
+      }
+      if (steal < 8) {
+        const int q2 = (xcd + steal) & 7;
+        j = queue_slots(q2) > 0 ? atomicAdd(&p.tile_ctr[q2], 1) : 0;
+      }
+    }
+    return -1;
+  };
 
-    // ---- M tile -> expert segment ----------------------------------------
-    int e = 0, row0 = 0, valid = 0;
-    int mnat = mt_glob;  // M tile index in expert order (MX exponent words are by M tile)
+  // ---- tile -> expert segment (uniform) ---------------------------------------
+  struct Tile {
+    int t, nt, e, row0, valid, mnat;  // t: M tile (-1: none); mnat: M tile in expert order
+  };
+  // (expert, first row, rows, MX M tile) of M tile m, from the routing tables
+  auto locate = [&, HK_CAP](int m, int& e, int& row0, int& valid, int& mnat) __attribute__((always_inline)) {
+    e = 0;
+    mnat = m;
     if (dense) {
-      row0 = mt_glob * kBM;
+      row0 = m * kBM;
       valid = static_cast<int>(min<int64_t>(kBM, p.rows - row0));
     } else if (p.mtile_list != nullptr) {
-      e = p.mtile_list[2 * mt_glob];
-      row0 = p.mtile_list[2 * mt_glob + 1];
+      e = p.mtile_list[2 * m];
+      row0 = p.mtile_list[2 * m + 1];
       valid = min(kBM, p.offsets[e + 1] - row0);
-      mnat = p.mtile_offsets[e] + (row0 - p.offsets[e]) / kBM;
+      if constexpr (kMX) mnat = p.mtile_offsets[e] + (row0 - p.offsets[e]) / kBM;
     } else {
-      int lo = 0, hi = p.num_experts;  // largest e with mtile_offsets[e] <= mt_glob
+      int lo = 0, hi = p.num_experts;  // largest e with mtile_offsets[e] <= m
       while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
-        if (p.mtile_offsets[mid] <= mt_glob) lo = mid; else hi = mid;
+        if (p.mtile_offsets[mid] <= m) lo = mid; else hi = mid;
       }
       e = lo;
-      row0 = p.offsets[e] + (mt_glob - p.mtile_offsets[e]) * kBM;
+      row0 = p.offsets[e] + (m - p.mtile_offsets[e]) * kBM;
       valid = min(kBM, p.offsets[e + 1] - row0);
     }
-    e = __builtin_amdgcn_readfirstlane(e);
-    row0 = __builtin_amdgcn_readfirstlane(row0);
-    mnat = __builtin_amdgcn_readfirstlane(mnat);
-    valid = __builtin_amdgcn_readfirstlane(valid);
+  };
+  auto uniform = [](int m, int n, int e, int row0, int valid, int mnat) __attribute__((always_inline)) {
+    Tile c{-1, 0, 0, 0, 0, 0};
+    c.t = __builtin_amdgcn_readfirstlane(m);
+    if (c.t < 0) return c;
+    c.nt = __builtin_amdgcn_readfirstlane(n);
+    c.e = __builtin_amdgcn_readfirstlane(e);
+    c.row0 = __builtin_amdgcn_readfirstlane(row0);
+    c.valid = __builtin_amdgcn_readfirstlane(valid);
+    c.mnat = __builtin_amdgcn_readfirstlane(mnat);
+    return c;
+  };
+  // the tile (m, n) published in LDS slots s, s + 1, located here
+  auto decode = [&, HK_CAP](int s) __attribute__((always_inline)) {
+    const int m = __builtin_amdgcn_readfirstlane(HK_SLOT[s]);
+    if (m < 0) return Tile{-1, 0, 0, 0, 0, 0};
+    int e, row0, valid, mnat;
+    locate(m, e, row0, valid, mnat);
+    return uniform(m, HK_SLOT[s + 1], e, row0, valid, mnat);
+  };
 
-    // B (group 0 only): LDS row 32*i + ld_row holds weight row b_row0 + boff(i)
-    //   plain: nt*256 + r                       -> boff(i) = 32*i
-    //   SiLU:  quarter q = r >> 6 = i >> 1 holds 32 gate rows (i even) then
-    //          the 32 matching up rows (i odd) -> boff(i) = 32*(i>>1) + (i&1)*I
-    // Row-major weights: lane offset of that row and chunk, K step kt at byte
-    // kt*128.  Packed weights: the tile's K step kt is the 32 KiB stage image
-    // at kt*32 KiB of the tile's own panel, so instruction i of wave wg reads
-    // the 1 KiB at (32*i + 8*wg)*128 linearly.
-    // Lane offsets of the two register halves of a B fragment within its
-    // 2 KiB of the stage: fragment-major (packed weights) or swizzled rows,
-    // in the K order of the MFMA variant (read_frag / read_frag_mx).
-    int b_lo, b_hi;
-    if (p.b_packed) {
-      if constexpr (kMX) {
-        b_lo = (lg & 1) * 1024 + ((lg >> 1) * 16 + l16) * 16;
-        b_hi = (lg & 1) * 1024 + (((lg >> 1) + 2) * 16 + l16) * 16;
-      } else {
-        b_lo = lane * 16;
-        b_hi = 1024 + lane * 16;
-      }
-    } else {
-      b_lo = l16 * kBK + ((kMX ? lg : 2 * lg) ^ fx) * 16;
-      b_hi = l16 * kBK + ((kMX ? lg + 4 : 2 * lg + 1) ^ fx) * 16;
-    }
-    i32x4 b_srd;
-    int b_voff, b_kstride;
-    if (p.b_packed) {
-      b_srd = make_srd(p.b + (static_cast<int64_t>(e) * (p.nb / kBN) + nt) * kBN * p.K,
-                       static_cast<uint32_t>(kBN) * p.K);
-      b_voff = wg * 8 * kBK + lane * 16;
-      b_kstride = kTileBytes;
-    } else {
-      b_srd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K, static_cast<uint32_t>(p.nb) * p.K);
-      const int b_row0 = kSilu ? nt * 128 + ld_row : nt * kBN + ld_row;
-      b_voff = b_row0 * p.K + ld_chunk * 16;
-      b_kstride = kBK;
-    }
-
-    // A (own half): LDS row grp*128 + 32*i + ld_row <- A row of output row
-    // row0 + min(r, valid - 1); 16-row sub-tiles past `valid` are not loaded.
-    int a_voff[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = row0 + min(wave_row0 + 32 * i + ld_row, valid - 1);
-      const int ar = p.a_gather ? p.a_gather[rr] / p.gather_div : rr;
-      a_voff[i] = ar * p.K + ld_chunk * 16;
-    }
-    // activation scales of the own half: waves 0,1 of each group gather 64 slots
-    const bool scale_loader = kBlockSc && wg < 2;
-    int as_voff = 0;
-    if (scale_loader) {
-      const int rr = row0 + min(scale_slot_row(wave_row0 + wg * 64 + lane), valid - 1);
-      const int ar = p.a_gather ? p.a_gather[rr] / p.gather_div : rr;
-      as_voff = static_cast<int>(ar * p.as_rs) * 4;
-    }
-    // MX: a tile's exponent words of one K step are 1 KiB contiguous per
-    // operand, so wave 0 DMAs all 256 A words and wave 1 all 256 B words (one
-    // 16-byte-per-lane instruction each), with group 0's A half.  Group 1 last
-    // read that stage's words three phases earlier (its first memory phase of
-    // the step before).  Words past the packed arrays read as zero (rows that
-    // are never stored).
-    const bool mx_loader = kMX && wave < 2;
-    i32x4 mx_srd;
-    int mx_voff = 0, mx_kstride = 0, mx_lds = 0;
+  // Lane offsets of the two register halves of a B fragment within its 2 KiB
+  // of the stage: fragment-major (packed weights) or swizzled rows, in the K
+  // order of the MFMA variant (read_frag / read_frag_mx).
+  int b_lo, b_hi;
+  if (p.b_packed) {
     if constexpr (kMX) {
-      const int k_steps_ = p.K / kBK;
+      b_lo = (lg & 1) * 1024 + ((lg >> 1) * 16 + l16) * 16;
+      b_hi = (lg & 1) * 1024 + (((lg >> 1) + 2) * 16 + l16) * 16;
+    } else {
+      b_lo = lane * 16;
+      b_hi = 1024 + lane * 16;
+    }
+  } else {
+    b_lo = l16 * kBK + ((kMX ? lg : 2 * lg) ^ fx) * 16;
+    b_hi = l16 * kBK + ((kMX ? lg + 4 : 2 * lg + 1) ^ fx) * 16;
+  }
+
+  // ---- per-tile DMA sources --------------------------------------------------
+  // B (group 0 rows 0-127, group 1 rows 128-255): LDS row 32*i + ld_row holds
+  // weight row b_row0 + boff(i)
+  //   plain: nt*256 + r                       -> boff(i) = 32*i
+  //   SiLU:  quarter q = r >> 6 = i >> 1 holds 32 gate rows (i even) then
+  //          the 32 matching up rows (i odd) -> boff(i) = 32*(i>>1) + (i&1)*I
+  // Row-major weights: lane offset of that row and chunk, K step kt at byte
+  // kt*128.  Packed weights: the tile's K step kt is the 32 KiB stage image at
+  // kt*32 KiB of the tile's own panel, so instruction i of wave wg reads the
+  // 1 KiB at (32*i + 8*wg)*128 linearly.
+  i32x4 b_srd;
+  int b_voff = 0, b_kstride = 0;
+#define HK_SET_B(c) b_source(p, (c).e, (c).nt, kSilu, wg, b_srd, b_voff, b_kstride)
+  // A (own half): LDS row grp*128 + 32*i + ld_row <- A row of output row
+  // row0 + min(r, valid - 1); 16-row sub-tiles past `valid` are not loaded.
+  // Gathered rows come straight from a_gather, or, for a tile prepared during
+  // the previous tile's K loop, from its row list in LDS (stage_rows).
+  // The activation-scale loaders (waves 0, 1 of each group, block scales)
+  // gather 64 slots of the own half; MX: wave 0 DMAs the tile's 256 A words of
+  // a K step (1 KiB), wave 1 its 256 B words, words past the packed arrays
+  // read as zero (rows that are never stored).
+  const bool scale_loader = kBlockSc && wg < 2;
+  const bool mx_loader = kMX && wave < 2;
+  int a_voff[4], as_voff = 0, mx_voff = 0, mx_kstride = 0, mx_lds = 0;
+  i32x4 mx_srd = {0, 0, 0, 0};
+  auto a_row = [&, HK_CAP](const Tile& c, int r, bool staged) __attribute__((always_inline)) -> int {
+    const int rc = min(r, c.valid - 1);
+    if (p.a_gather == nullptr) return c.row0 + rc;
+    return (staged ? HK_NROW[rc] : p.a_gather[c.row0 + rc]) / p.gather_div;
+  };
+  auto set_a = [&, HK_CAP](const Tile& c, bool staged) __attribute__((always_inline)) {
+    // lane constants recomputed here (once per tile)
+    const int ln = lane_here();
+    const int lrow = 8 * wg + (ln >> 3), lchunk = (ln & 7) ^ swz(lrow);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a_voff[i] = a_row(c, wave_row0 + 32 * i + lrow, staged) * p.K + lchunk * 16;
+    if (scale_loader)
+      as_voff = static_cast<int>(a_row(c, scale_slot_row(wave_row0 + wg * 64 + ln), staged) * p.as_rs) * 4;
+    if constexpr (kMX) {
       if (wave == 0) {
-        mx_srd = make_srd(p.a_scale, static_cast<uint32_t>(k_steps_ * p.as_rs * 4));
-        mx_voff = (mnat * kBM + lane * 4) * 4;
+        mx_srd = make_srd(p.a_scale, static_cast<uint32_t>(k_steps * p.as_rs * 4));
+        mx_voff = (c.mnat * kBM + ln * 4) * 4;
         mx_kstride = static_cast<int>(p.as_rs) * 4;
         mx_lds = 2 * kTileBytes;
-      } else if (dense) {
-        mx_srd = make_srd(p.b_scale, static_cast<uint32_t>(k_steps_ * p.nb * 4));
-        mx_voff = (nt * kBN + lane * 4) * 4;
-        mx_kstride = p.nb * 4;
-        mx_lds = 2 * kTileBytes + kScaleBytes;
-      } else {
-        // this B tile's words: k_steps_ consecutive KiB
-        const int ntiles = p.nb / kBN;
-        mx_srd = make_srd(reinterpret_cast<const uint8_t*>(p.b_scale) +
-                              (static_cast<int64_t>(e) * ntiles + nt) * k_steps_ * 1024,
-                          static_cast<uint32_t>(k_steps_) * 1024);
-        mx_voff = lane * 16;
-        mx_kstride = 1024;
+      } else if (wave == 1) {
+        if (dense) {
+          mx_srd = make_srd(p.b_scale, static_cast<uint32_t>(k_steps * p.nb * 4));
+          mx_voff = (c.nt * kBN + ln * 4) * 4;
+          mx_kstride = p.nb * 4;
+        } else {
+          // this B tile's words: k_steps consecutive KiB
+          const int ntiles = p.nb / kBN;
+          mx_srd = make_srd(reinterpret_cast<const uint8_t*>(p.b_scale) +
+                                (static_cast<int64_t>(c.e) * ntiles + c.nt) * k_steps * 1024,
+                            static_cast<uint32_t>(k_steps) * 1024);
+          mx_voff = ln * 16;
+          mx_kstride = 1024;
+        }
         mx_lds = 2 * kTileBytes + kScaleBytes;
       }
     }
+  };
+  // The next tile's gathered rows into LDS: waves 0-3, 64 row indices each.
+  auto stage_rows = [&, HK_CAP](const Tile& c) __attribute__((always_inline)) {
+    if (p.a_gather != nullptr && wave < 4) {
+      const i32x4 g_srd = make_srd(p.a_gather, 0xffffffffu);
+      load_lds_4B(g_srd, HK_NROW + 64 * wave, (c.row0 + min(64 * wave + lane_here(), c.valid - 1)) * 4, 0);
+    }
+  };
+  // A tile's weight scales for every K step into buffer `buf`: waves 0-3, one
+  // column block (gate / first, up / second) and 64 K steps each; steps past
+  // K read as zero.
+  auto stage_bscales = [&, HK_CAP](const Tile& c, int buf) __attribute__((always_inline)) {
+    if constexpr (kBlockSc) {
+      const int h = wave & 1, part = wave >> 1;
+      if (wave < 4 && part * 64 < k_steps) {
+        const int nbh = h ? (kSilu ? p.n_out / kGroup + c.nt : 2 * c.nt + 1) : (kSilu ? c.nt : 2 * c.nt);
+        const float* src = p.b_scale + (static_cast<int64_t>(c.e) * (p.nb / kGroup) + nbh) * k_steps;
+        const i32x4 srd = make_srd(src, static_cast<uint32_t>(k_steps) * 4);
+        load_lds_4B(srd, HK_BS + (buf * 2 + h) * kMaxKBlocks + part * 64, (part * 64 + lane_here()) * 4, 0);
+      }
+    }
+  };
 
-    // DMA instructions of one K step issued by this wave.  issue_a: its
-    // group's A half (4, dead 16-row sub-tiles skipped) and, for waves 0-1 of
-    // each group, the activation scales (1).  issue_b: exactly 4 loads, half
-    // of the B stage (group 0 rows 0-127, group 1 rows 128-255); being the
-    // last 4 loads a wave issues, they are what vmcnt(4) leaves in flight.
-    auto issue_a = [&](int kt) {
-      uint8_t* sa = smem + (kt & 1) * kStg;
-      const int koff = kt * kBK;
+  // DMA instructions of one K step issued by this wave.  issue_a: its group's
+  // A half of K step kt of a tile of `valid` rows into stage stg (4, dead
+  // 16-row sub-tiles skipped) and, for the scale / MX loaders, one more.
+  // issue_b: exactly 4 loads, half of the B stage (group 0 rows 0-127, group 1
+  // rows 128-255); being the last 4 loads a wave issues in a K step, they are
+  // what vmcnt(4) leaves in flight.
+  auto issue_a = [&, HK_CAP](int kt, int stg, int valid) __attribute__((always_inline)) {
+    uint8_t* sa = smem + stg * kStg;
+    const int koff = kt * kBK;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r8 = wave_row0 + 32 * q + 8 * wg;  // first row of this wave load
-        if ((r8 & ~15) < valid) load_lds_16B(a_srd, sa + r8 * kBK, a_voff[q], koff);
-      }
-      if (scale_loader) {
-        const i32x4 as_srd = make_srd(p.a_scale, 0xffffffffu);
-        load_lds_4B(as_srd, sa + 2 * kTileBytes + (wave_row0 + wg * 64) * 4, as_voff,
-                    static_cast<int>(kt * p.as_ks) * 4);
-      }
-      if (mx_loader) load_lds_16B(mx_srd, sa + mx_lds, mx_voff, kt * mx_kstride);
-    };
-    auto issue_b = [&](int kt) {
-      uint8_t* sb = smem + (kt & 1) * kStg + kTileBytes;
+    for (int q = 0; q < 4; ++q) {
+      const int r8 = wave_row0 + 32 * q + 8 * wg;  // first row of this wave load
+      if ((r8 & ~15) < valid) load_lds_16B(a_srd, sa + r8 * kBK, a_voff[q], koff);
+    }
+    if (scale_loader) {
+      const i32x4 as_srd = make_srd(p.a_scale, 0xffffffffu);
+      load_lds_4B(as_srd, sa + 2 * kTileBytes + (wave_row0 + wg * 64) * 4, as_voff,
+                  static_cast<int>(kt * p.as_ks) * 4);
+    }
+    if (mx_loader) load_lds_16B(mx_srd, sa + mx_lds, mx_voff, kt * mx_kstride);
+  };
+  auto issue_b = [&, HK_CAP](int kt, int stg) __attribute__((always_inline)) {
+    uint8_t* sb = smem + stg * kStg + kTileBytes;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int i = grp * 4 + q;
-        const int boff = kSilu ? (32 * (i >> 1) + ((i & 1) ? p.n_out : 0)) : 32 * i;
-        const int ioff = p.b_packed ? 32 * i * kBK : boff * p.K;
-        load_lds_16B(b_srd, sb + (32 * i + 8 * wg) * kBK, b_voff, kt * b_kstride + ioff);
-      }
-    };
-    // every load of this wave except its last issue_b has completed
-    auto wait_dma = [&](bool b_in_flight) {
-      if (b_in_flight) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    };
+    for (int q = 0; q < 4; ++q) {
+      const int i = grp * 4 + q;
+      const int boff = kSilu ? (32 * (i >> 1) + ((i & 1) ? p.n_out : 0)) : 32 * i;
+      const int ioff = p.b_packed ? 32 * i * kBK : boff * p.K;
+      load_lds_16B(b_srd, sb + (32 * i + 8 * wg) * kBK, b_voff, kt * b_kstride + ioff);
+    }
+  };
+  // every load of this wave except its last issue_b has completed
+  auto wait_dma = [&, HK_CAP](bool b_in_flight) __attribute__((always_inline)) {
+    if (b_in_flight) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  // a tile's first two stages (steps 0 and 1 at global steps gs, gs + 1) and
+  // its weight scales, when the previous tile did not prepare them
+  auto start_tile = [&, HK_CAP](const Tile& c, int buf, int gs) __attribute__((always_inline)) {
+    HK_SET_B(c);
+    set_a(c, false);
+    stage_bscales(c, buf);
+    issue_a(0, gs & 1, c.valid);
+    issue_b(0, gs & 1);
+    if (k_steps > 1) issue_b(1, (gs + 1) & 1);
+    wait_dma(k_steps > 1);  // stage 0 and the weight scales visible to all
+  };
+
+  // The next tile is found during a tile's K loop by thread 0, one memory
+  // round trip per K step, each looked at only after the step's own DMA wait
+  // (which covers it): step 1 claims a slot, its end turns the slot into
+  // (m, n) and loads the M tile's (expert, first row); step 2's end loads the
+  // expert's row offsets; step 3's end publishes the tile in LDS.  Step
+  // k_steps - 3 reads it and DMAs its gathered rows and weight scales into
+  // LDS; its first stages are loaded by the last K steps like any other step:
+  // B(0) at step k_steps - 2, A(0) and B(1) at k_steps - 1.  Stage parity runs
+  // on a global step count, so it continues across tiles.  With fewer than 8
+  // K steps each tile starts on its own after the previous epilogue.
+  const bool pipe = k_steps >= 8;
+  if (tid == 0) {
+    int n = 0;
+    HK_SLOT[0] = claim_end(claim_start(), n);
+    HK_SLOT[1] = n;
+  }
+  __syncthreads();
+  Tile cur = decode(0);
+  if (cur.t < 0) return;
+  int buf = 0, gstep = 0;
+  start_tile(cur, buf, gstep);
+
+  while (true) {
+    if (grp == 1) sync_lds();  // group 1 runs one phase behind group 0
+    const float* bsl = HK_BS + buf * 2 * kMaxKBlocks;
+    const int live_sub = max(0, min(8, (cur.valid - wave_row0 + 15) >> 4));
+    Tile nxt{-1, 0, 0, 0, 0, 0};
+    // thread 0's lookups of the next tile (meaningful in lane 0 only)
+    int q_j = 0, q_m = -1, q_n = 0, q_e = 0, q_row0 = 0, q_end = 0, q_beg = 0, q_mt = 0;
 
     f32x4 acc[8][4];
 #pragma unroll
@@ -478,29 +597,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int live_sub = max(0, min(8, (valid - wave_row0 + 15) >> 4));
-
-    __syncthreads();  // previous tile is done with every LDS buffer
-    if constexpr (kBlockSc) {
-      // weight scales of this tile for every K block: [2][k_steps]
-      const float* bs = p.b_scale + static_cast<int64_t>(e) * (p.nb / kGroup) * k_steps;
-      const int nb0 = kSilu ? nt : 2 * nt;                           // gate / first n block
-      const int nb1 = kSilu ? (p.n_out / kGroup + nt) : 2 * nt + 1;  // up / second n block
-      for (int t = tid; t < 2 * k_steps; t += kThreads) {
-        const int h = t >= k_steps;
-        bs_lds[t] = bs[(h ? nb1 : nb0) * k_steps + (t - h * k_steps)];
-      }
-    }
-    issue_a(0);
-    issue_b(0);
-    if (k_steps > 1) issue_b(1);
-    wait_dma(k_steps > 1);     // stage 0 (and the weight scales) visible to all
-    if (grp == 1) sync_lds();  // group 1 runs one phase behind group 0
-
-    // block scales of the current K step: the activation scale of each of the
-    // lane's 8 sub-tile rows, and the weight scale of its gate / up (or only)
-    // 128-column block
-    float sa_cur[8], sb_cur0 = 1.0f, sb_cur1 = 1.0f;
+    // block scales of the current K step: the activation scales of the lane's 4
+    // sub-tile rows of the coming compute phase, and the weight scale of its
+    // gate / up (or only) 128-column block
+    float sa_cur[4], sb_cur0 = 1.0f, sb_cur1 = 1.0f;
 
     // Four barrier-separated phases per K step: memory (LDS fragment reads,
     // DMA issue), compute (MFMAs from registers only), memory, compute.  Group
@@ -514,10 +614,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     // loads but the newest B(kt+2) before the barrier ending phase 4kt+3
     // (group 0: end of its second compute phase; group 1: end of its second
     // memory phase).
-    for (int kt = 0; kt < k_steps; ++kt) {
-      const bool more = kt + 1 < k_steps;
-      const uint8_t* sa = smem + (kt & 1) * kStg;
+    // One K step.  kPlain: this tile's loads only (A(kt+1), B(kt+2) while
+    // they exist); with pipelining, kClaim / kLookup / kPublish: steps 1-3,
+    // which find the next tile (thread 0); kStage: step k_steps-3, which reads
+    // it and stages its rows and weight scales; kNextB0: step k_steps-2, whose
+    // B load is the next tile's B(0) and which sets up the next tile's A
+    // sources; kNextA0: the last step, whose loads are the next tile's A(0) and
+    // B(1).  The steps with next-tile work are separate copies, so the loop of
+    // plain steps keeps the registers of a single tile.
+    auto step = [&, HK_CAP](int kt, auto mode_tag) __attribute__((always_inline)) {
+      constexpr int MODE = decltype(mode_tag)::value;
+      const int stg = (gstep + kt) & 1;
+      const uint8_t* sa = smem + stg * kStg;
       const uint8_t* sb = sa + kTileBytes;
+      if constexpr (MODE == kNextA0) {
+        // first thing: the next tile's A(0) (its sources were set a step ago)
+        // into the previous step's stage, whose reads all ended with that step
+        if (nxt.t >= 0) issue_a(0, stg ^ 1, nxt.valid);
+      }
+      if constexpr (MODE == kClaim) {
+        if (tid == 0) q_j = claim_start();
+      }
 
       // ---- memory phase 1: B fragments, A sub-tiles 0-3, scales, DMA kt+1
       i32x8 bf[4], af[4];
@@ -543,25 +660,39 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         for (int i = 0; i < 4; ++i) af[i] = read_operand<kMX>(sa, wave_row0 + i * 16 + l16, lg, fx);
       }
       if constexpr (kBlockSc) {
-        // this step's scales; the factors are formed in the compute phases
-        const float* sc = reinterpret_cast<const float*>(sb + kTileBytes) + wave_row0 + l16 * 8;
-        const f32x4 s_lo = *reinterpret_cast<const f32x4*>(sc);
-        const f32x4 s_hi = *reinterpret_cast<const f32x4*>(sc + 4);
+        // this step's scales of sub-tiles 0-3 (4-7 in the second memory phase);
+        // the factors are formed in the compute phases
+        const f32x4 s_lo = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(sb + kTileBytes) +
+                                                           wave_row0 + l16 * 8);
         sa_cur[0] = s_lo.x; sa_cur[1] = s_lo.y; sa_cur[2] = s_lo.z; sa_cur[3] = s_lo.w;
-        sa_cur[4] = s_hi.x; sa_cur[5] = s_hi.y; sa_cur[6] = s_hi.z; sa_cur[7] = s_hi.w;
         if constexpr (kSilu) {
-          sb_cur0 = bs_lds[kt];
-          sb_cur1 = bs_lds[k_steps + kt];
+          sb_cur0 = bsl[kt];
+          sb_cur1 = bsl[kMaxKBlocks + kt];
         } else {
-          sb_cur0 = sb_cur1 = bs_lds[(wg >> 1) * k_steps + kt];
+          sb_cur0 = sb_cur1 = bsl[(wg >> 1) * kMaxKBlocks + kt];
         }
       }
-      if (more) issue_a(kt + 1);
+      if constexpr (MODE != kNextA0) {
+        if (MODE != kPlain || kt + 1 < k_steps) issue_a(kt + 1, stg ^ 1, cur.valid);
+      }
+      if constexpr (MODE == kStage) {
+        // the next tile, published at step 3: its rows and weight scales into LDS
+        nxt = uniform(HK_SLOT[2], HK_SLOT[3], HK_SLOT[4], HK_SLOT[5], HK_SLOT[6], HK_SLOT[7]);
+        if (nxt.t >= 0) {
+          stage_rows(nxt);
+          stage_bscales(nxt, buf ^ 1);
+        }
+      }
+      if constexpr (MODE == kNextB0) {
+        // this tile's last A load is issued: the A sources become the next tile's
+        // (its rows were staged a step ago)
+        if (nxt.t >= 0) set_a(nxt, true);
+      }
       sync_lds();
       __builtin_amdgcn_sched_barrier(0);
 
       // ---- compute phase 1: sub-tiles 0-3
-      auto compute = [&](int i0) {
+      auto compute = [&, HK_CAP](int i0) __attribute__((always_inline)) {
         __builtin_amdgcn_s_setprio(1);
         // Skipped only when all four sub-tiles are dead; a partly live phase
         // also computes its dead sub-tiles (stale fragments, never stored).
@@ -573,24 +704,29 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
             mx_subtile<2>(acc[i0 + 2], bf, af[2], mx_sb, sa_w);
             mx_subtile<3>(acc[i0 + 3], bf, af[3], mx_sb, sa_w);
           } else if constexpr (kBlockSc) {
-            // factor of sub-tile u: its row's activation scale times the
-            // weight scale of the column block (gate: j < 2, up: j >= 2)
-            float f0[4], f1[4];
+            // MFMA t from zero; the FMAs folding MFMA t-2 into its accumulator
+            // follow it, so they run while MFMA t occupies the matrix core and
+            // read a result two MFMAs old (folding the previous MFMA's result
+            // stalls on it: about 44 instead of 38 cycles per MFMA).  The order
+            // is pinned with scheduling groups.  Factor of sub-tile u: its row's
+            // activation scale times the weight scale of the column block
+            // (gate: j < 2, up: j >= 2), formed before its first fold.
+            f32x4 pr[3];
+            float f0 = 0.0f, f1 = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              f0[u] = sa_cur[i0 + u] * sb_cur0;
-              f1[u] = kSilu ? sa_cur[i0 + u] * sb_cur1 : f0[u];
-            }
-            // MFMA t from zero; the FMAs of MFMA t-1 follow it, so they run
-            // while MFMA t occupies the matrix core
-            f32x4 prev = mfma_e4m3_16x16x128(bf[0], af[0], f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-            for (int t = 1; t <= 16; ++t) {
-              f32x4 cur;
-              if (t < 16) cur = mfma_e4m3_16x16x128(bf[t & 3], af[t >> 2], f32x4{0.f, 0.f, 0.f, 0.f});
-              const int u = (t - 1) >> 2, j = (t - 1) & 3;
-              fold_block(acc[i0 + u][j], prev, (kSilu && j >= 2) ? f1[u] : f0[u]);
-              if (t < 16) prev = cur;
+            for (int t = 0; t < 18; ++t) {
+              if (t < 16) pr[t % 3] = mfma_e4m3_16x16x128(bf[t & 3], af[t >> 2], f32x4{0.f, 0.f, 0.f, 0.f});
+              if (t >= 2) {
+                const int u = (t - 2) >> 2, j = (t - 2) & 3;
+                if (j == 0) {
+                  f0 = sa_cur[u] * sb_cur0;
+                  f1 = kSilu ? sa_cur[u] * sb_cur1 : f0;
+                }
+                fold_block(acc[i0 + u][j], pr[(t - 2) % 3], (kSilu && j >= 2) ? f1 : f0);
+              }
+              if (t < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA, then the VALU
+              if (t >= 2 && ((t - 2) & 3) == 0) __builtin_amdgcn_sched_group_barrier(0x002, kSilu ? 6 : 5, 0);
+              if (t >= 2 && ((t - 2) & 3) != 0) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
             }
           } else {
 #pragma unroll
@@ -607,195 +743,306 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
 
-      // ---- memory phase 2: A sub-tiles 4-7
+      // ---- memory phase 2: A sub-tiles 4-7 and their scales, B two steps
+      // ahead (the next tile's B(0) / B(1) at the last two steps)
+      if constexpr (kBlockSc) {
+        const f32x4 s_hi = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(sb + kTileBytes) +
+                                                           wave_row0 + l16 * 8 + 4);
+        sa_cur[0] = s_hi.x; sa_cur[1] = s_hi.y; sa_cur[2] = s_hi.z; sa_cur[3] = s_hi.w;
+      }
       if (live_sub > 4) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[i] = read_operand<kMX>(sa, wave_row0 + (i + 4) * 16 + l16, lg, fx);
       }
-      const bool more2 = kt + 2 < k_steps;
-      if (more2) issue_b(kt + 2);
-      if (grp == 1) wait_dma(more2); else sync_lds();
+      bool b_fly = false;
+      if constexpr (MODE == kNextB0 || MODE == kNextA0) {
+        if (nxt.t >= 0) {
+          if constexpr (MODE == kNextB0) HK_SET_B(nxt);  // this tile's B loads are done
+          issue_b(MODE == kNextB0 ? 0 : 1, stg);
+          b_fly = true;
+        }
+      } else if (MODE != kPlain || kt + 2 < k_steps) {
+        issue_b(kt + 2, stg);
+        b_fly = true;
+      }
+      if (grp == 1) wait_dma(b_fly); else sync_lds();
       __builtin_amdgcn_sched_barrier(0);
 
       // ---- compute phase 2: sub-tiles 4-7
       compute(4);
       __builtin_amdgcn_sched_barrier(0);
-      if (grp == 0) wait_dma(more2); else __builtin_amdgcn_s_barrier();
+      if (grp == 0) wait_dma(b_fly); else __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
+
+      // thread 0's lookups: each result was covered by this step's DMA wait
+      if constexpr (MODE == kClaim) {
+        if (tid == 0) {
+          q_m = claim_end(q_j, q_n);
+          if (q_m >= 0 && !dense && p.mtile_list != nullptr) {
+            q_e = p.mtile_list[2 * q_m];
+            q_row0 = p.mtile_list[2 * q_m + 1];
+          }
+        }
+      } else if constexpr (MODE == kLookup) {
+        if (tid == 0 && q_m >= 0 && !dense && p.mtile_list != nullptr) {
+          q_end = p.offsets[q_e + 1];
+          if constexpr (kMX) {
+            q_beg = p.offsets[q_e];
+            q_mt = p.mtile_offsets[q_e];
+          }
+        }
+      } else if constexpr (MODE == kPublish) {
+        // read at step k_steps - 3 >= 5, after this step's barriers
+        if (tid == 0) {
+          int e = q_e, row0 = q_row0, valid = 0, mnat = q_m;
+          if (q_m >= 0) {
+            if (!dense && p.mtile_list != nullptr) {
+              valid = min(kBM, q_end - row0);
+              if constexpr (kMX) mnat = q_mt + (row0 - q_beg) / kBM;
+            } else {
+              locate(q_m, e, row0, valid, mnat);
+            }
+          }
+          HK_SLOT[2] = q_m; HK_SLOT[3] = q_n; HK_SLOT[4] = e;
+          HK_SLOT[5] = row0; HK_SLOT[6] = valid; HK_SLOT[7] = mnat;
+        }
+      }
+    };
+    if (pipe) {
+      step(0, std::integral_constant<int, kPlain>{});
+      step(1, std::integral_constant<int, kClaim>{});
+      step(2, std::integral_constant<int, kLookup>{});
+      step(3, std::integral_constant<int, kPublish>{});
+      for (int kt = 4; kt < k_steps - 3; ++kt) step(kt, std::integral_constant<int, kPlain>{});
+      step(k_steps - 3, std::integral_constant<int, kStage>{});
+      step(k_steps - 2, std::integral_constant<int, kNextB0>{});
+      step(k_steps - 1, std::integral_constant<int, kNextA0>{});
+    } else {
+      for (int kt = 0; kt < k_steps; ++kt) step(kt, std::integral_constant<int, kPlain>{});
     }
     if (grp == 0) sync_lds();  // group 0's extra barrier pairs with group 1's first
+    // without pipelining the next tile is claimed now and started after the epilogue
+    if (!pipe) {
+      if (tid == 0) {
+        int n = 0;
+        HK_SLOT[0] = claim_end(claim_start(), n);
+        HK_SLOT[1] = n;
+      }
+      __syncthreads();
+      nxt = decode(0);
+    }
 
-    // ---- epilogue ----------------------------------------------------------
+    // ---- epilogue ------------------------------------------------------------
     // lane holds, for sub-tile i and n fragment j, output row wave_row0+16i+l16
-    // and columns 16*j + 4*lg .. +3 of the wave's 64-column quarter
+    // and columns 16*j + 4*lg .. +3 of the wave's 64-column quarter; for the
+    // SiLU epilogues fragments j and j+2 are the gate and up columns of h
+    // columns 32*wg + 16*j + 4*lg .. +3 of the tile's 128.
+    // `ct`: the A half of the last K step's stage (32 KiB), free until the next
+    // tile's step 0 DMAs A(1) into it; output tiles are staged there and stored
+    // as 16-byte chunks that cover whole rows.  Rows of 16-byte chunks; chunk c
+    // of row r sits at slot c ^ (r mod the row's chunk count), so both the
+    // fragment-shaped writes and the row-shaped reads spread over the banks.
+    uint8_t* ct = smem + ((gstep + k_steps - 1) & 1) * kStg;
+    const int row0 = cur.row0, valid = cur.valid, nt = cur.nt;
+    // lane position recomputed here, so its address terms are not kept live
+    // from the kernel's start
+    const int eln = lane_here(), el16 = eln & 15, elg = eln >> 4;
     // per-tensor scales are applied here; block-scaled and MX accumulators
     // already hold the scaled sums
     float tens = 1.0f;
     if constexpr (SC == Scale::kTensor)
-      tens = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[e] : 1.0f);
-    auto fac = [&](int, int) -> float { return tens; };
+      tens = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[cur.e] : 1.0f);
 
-    if constexpr (EPI == Epi::kStoreF32) {
+    if constexpr (EPI == Epi::kStoreBf16) {
+      // four rounds of 64 rows: sub-tiles 2q, 2q+1 of both halves (LDS row
+      // rr = 32*grp + 16*(i - 2q) + l16, 512 bytes = 32 chunks)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (32 * q >= valid) break;  // uniform: no row of this round or later is stored
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int i = 2 * q + h, rr = grp * 32 + h * 16 + el16;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = wg * 8 + 2 * j + (elg >> 1);
+            uint2 v;
+            v.x = pack_bf16x2(acc[i][j][0] * tens, acc[i][j][1] * tens);
+            v.y = pack_bf16x2(acc[i][j][2] * tens, acc[i][j][3] * tens);
+            *reinterpret_cast<uint2*>(ct + rr * 512 + ((c ^ (rr & 31)) << 4) + (elg & 1) * 8) = v;
+          }
+        }
+        sync_lds();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int idx = wave * 64 + eln + kThreads * u, rr = idx >> 5, c = idx & 31;
+          const int r = (rr >> 5) * 128 + 32 * q + (rr & 31);
+          if (r < valid) {
+            const uint4 v = *reinterpret_cast<const uint4*>(ct + rr * 512 + ((c ^ (rr & 31)) << 4));
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out +
+                                      nt * kBN + c * 8) = v;
+          }
+        }
+        sync_lds();
+      }
+    } else if constexpr (EPI == Epi::kStoreF32) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int r = wave_row0 + i * 16 + l16;
         if (i < live_sub && r < valid) {
-          const float f = fac(i, 0);
-          float* crow = static_cast<float*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * kBN + wg * 64;
+          const int64_t off = static_cast<int64_t>(row0 + r) * p.n_out + nt * kBN + wg * 64 + lg * 4;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             float4 v;
-            v.x = acc[i][j][0] * f; v.y = acc[i][j][1] * f;
-            v.z = acc[i][j][2] * f; v.w = acc[i][j][3] * f;
-            *reinterpret_cast<float4*>(crow + j * 16 + lg * 4) = v;
+            v.x = acc[i][j][0] * tens; v.y = acc[i][j][1] * tens;
+            v.z = acc[i][j][2] * tens; v.w = acc[i][j][3] * tens;
+            *reinterpret_cast<float4*>(static_cast<float*>(p.c) + off + j * 16) = v;
           }
         }
       }
     } else {
-      // stage the bf16 tile in LDS, then write whole rows with 16-byte stores
-      constexpr int ld = kSilu ? kCtLdSilu : kCtLdStore;
-      uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
-      __syncthreads();  // every wave is done reading the stages
+      // h = bf16(SiLU(gate) * up): lane's 8 values of sub-tile i (h columns
+      // 32*wg + 16*j + 4*lg .. +3 of row wave_row0 + 16i + l16, j = 0, 1)
+      auto h_of = [&, HK_CAP](int i, int j) __attribute__((always_inline)) -> uint2 {
+        float hv[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i < live_sub) {
-          uint16_t* crow = ct + (wave_row0 + i * 16 + l16) * ld;
-          if constexpr (kSilu) {
-            const float fg = fac(i, 0), fu = fac(i, 1);
+        for (int q = 0; q < 4; ++q) hv[q] = silu(acc[i][j][q] * tens) * (acc[i][j + 2][q] * tens);
+        return uint2{pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3])};
+      };
+      auto absmax = [](uint2 v) __attribute__((always_inline)) -> float {
+        return fmaxf(fmaxf(fabsf(bf16_bits_to_f32(v.x & 0xffffu)), fabsf(bf16_bits_to_f32(v.x >> 16))),
+                     fmaxf(fabsf(bf16_bits_to_f32(v.y & 0xffffu)), fabsf(bf16_bits_to_f32(v.y >> 16))));
+      };
+      // max |h| of the row over the wave's 32 columns (the 4 lane groups lg)
+      auto wave_row_max = [](float m) __attribute__((always_inline)) -> float {
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        return fmaxf(m, __shfl_xor(m, 32, 64));
+      };
+      auto hcol = [&, HK_CAP](int j) __attribute__((always_inline)) { return nt * 128 + wg * 32 + j * 16 + lg * 4; };
+      if constexpr (EPI == Epi::kSiluBf16) {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = wave_row0 + i * 16 + l16;
+          if (i < live_sub && r < valid) {
+            uint16_t* dst = static_cast<uint16_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-              float hv[4];
-#pragma unroll
-              for (int q = 0; q < 4; ++q) hv[q] = silu(acc[i][j][q] * fg) * (acc[i][j + 2][q] * fu);
-              uint2 v;
-              v.x = pack_bf16x2(hv[0], hv[1]);
-              v.y = pack_bf16x2(hv[2], hv[3]);
-              *reinterpret_cast<uint2*>(crow + wg * 32 + j * 16 + lg * 4) = v;
-            }
-          } else {
-            const float f = fac(i, 0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              uint2 v;
-              v.x = pack_bf16x2(acc[i][j][0] * f, acc[i][j][1] * f);
-              v.y = pack_bf16x2(acc[i][j][2] * f, acc[i][j][3] * f);
-              *reinterpret_cast<uint2*>(crow + wg * 64 + j * 16 + lg * 4) = v;
+              const uint2 v = h_of(i, j);
+              *reinterpret_cast<uint2*>(dst + hcol(j)) = v;
+              m = fmaxf(m, absmax(v));
             }
           }
         }
-      }
-      __syncthreads();
-      if constexpr (EPI == Epi::kStoreBf16) {
-        // 32 x 16-byte chunks per 256-column row
-        const int c = tid & 31;
-        for (int r = tid >> 5; r < valid; r += kThreads / 32) {
-          const uint4 v = *reinterpret_cast<const uint4*>(ct + r * ld + c * 8);
-          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out +
-                                    nt * kBN + c * 8) = v;
-        }
-      } else {
-        // two threads per row, 64 columns each
-        const int r = tid >> 1, half = tid & 1;
-        const uint16_t* src = ct + r * ld + half * 64;
-        float m = 0.0f;
-        if (r < valid) {
+        m = wave_max(m);
+        if (lane == 0 && p.amax != nullptr)
+          atomicMax(reinterpret_cast<unsigned int*>(p.amax), __float_as_uint(m));
+      } else if constexpr (EPI == Epi::kSiluMx) {
+        // MX requantisation of h: per row and 32-column block (the wave's 32
+        // columns), e = exponent field of amax (clamped to 254), q =
+        // e4m3(h * 2^(127-e)) (the quant_mx_kernel rule).  The tile's 128
+        // columns are one K step (nt) of the next GEMM; the block exponents of
+        // its rows are collected in LDS and written as that GEMM's packed words
+        // of M tile mnat (word q, byte g: row 64*(q/64) + 16g + q%16, block
+        // (q%64)/16).
+        uint8_t* ex = smem + kEpiOff;  // [256 rows][4 blocks]
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const uint4 v = *reinterpret_cast<const uint4*>(src + u * 8);
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(w[q] & 0xffffu)), fabsf(bf16_bits_to_f32(w[q] >> 16))));
-          }
-        }
-        if constexpr (EPI == Epi::kSiluBf16) {
-          if (r < valid) {
-            uint16_t* dst = static_cast<uint16_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * 128 + half * 64;
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-              *reinterpret_cast<uint4*>(dst + u * 8) = *reinterpret_cast<const uint4*>(src + u * 8);
-          }
-          m = wave_max(m);
-          if (lane == 0 && p.amax != nullptr)
-            atomicMax(reinterpret_cast<unsigned int*>(p.amax), __float_as_uint(m));
-        } else if constexpr (EPI == Epi::kSiluMx) {
-          // MX requantisation of the bf16 h: per row and 32-column block,
-          // e = exponent field of amax (clamped to 254), q = e4m3(h * 2^(127-e))
-          // (the quant_mx_kernel rule).  The tile's 128 columns are one K step
-          // (nt) of the next GEMM; the block exponents of its rows are gathered
-          // in LDS and written as that GEMM's packed words of M tile mnat
-          // (word q, byte g: row 64*(q/64) + 16g + q%16, block (q%64)/16).
-          uint8_t* ex = smem + kBM * kCtLdSilu * 2;  // [256 rows][4 blocks]
-          uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * 128 + half * 64;
-#pragma unroll
-          for (int b = 0; b < 2; ++b) {
-            uint32_t ebits = 0;
+        for (int i = 0; i < 8; ++i) {
+          const int r = wave_row0 + i * 16 + l16;
+          uint32_t ebits = 0;
+          if (i < live_sub) {
+            const uint2 h0 = h_of(i, 0), h1 = h_of(i, 1);
+            const float am = wave_row_max(fmaxf(absmax(h0), absmax(h1)));
             if (r < valid) {
-              uint4 v[4];
-              float am = 0.0f;
-#pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                v[u] = *reinterpret_cast<const uint4*>(src + b * 32 + u * 8);
-                const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                  am = fmaxf(am, fmaxf(fabsf(bf16_bits_to_f32(w[q] & 0xffffu)), fabsf(bf16_bits_to_f32(w[q] >> 16))));
-              }
               ebits = min((__float_as_uint(am) >> 23) & 0xffu, 254u);
               const int sh = 127 - static_cast<int>(ebits);
               auto qv = [&](uint32_t h) { return __builtin_amdgcn_ldexpf(bf16_bits_to_f32(h), sh); };
-              uint32_t qw[8];
-#pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                qw[2 * u] = pack_e4m3x4(qv(v[u].x & 0xffffu), qv(v[u].x >> 16), qv(v[u].y & 0xffffu), qv(v[u].y >> 16));
-                qw[2 * u + 1] = pack_e4m3x4(qv(v[u].z & 0xffffu), qv(v[u].z >> 16), qv(v[u].w & 0xffffu), qv(v[u].w >> 16));
-              }
-              *reinterpret_cast<uint4*>(dst + b * 32) = uint4{qw[0], qw[1], qw[2], qw[3]};
-              *reinterpret_cast<uint4*>(dst + b * 32 + 16) = uint4{qw[4], qw[5], qw[6], qw[7]};
+              uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out;
+              *reinterpret_cast<uint32_t*>(dst + hcol(0)) =
+                  pack_e4m3x4(qv(h0.x & 0xffffu), qv(h0.x >> 16), qv(h0.y & 0xffffu), qv(h0.y >> 16));
+              *reinterpret_cast<uint32_t*>(dst + hcol(1)) =
+                  pack_e4m3x4(qv(h1.x & 0xffffu), qv(h1.x >> 16), qv(h1.y & 0xffffu), qv(h1.y >> 16));
             }
-            ex[r * 4 + half * 2 + b] = static_cast<uint8_t>(ebits);  // 0 for rows past valid
           }
-          __syncthreads();
-          if (tid < kBM) {
-            const int q = tid;
-            const int rr = (q & ~63) + (q & 15), ks = (q >> 4) & 3;
-            uint32_t w = 0;
+          if (lg == 0) ex[r * 4 + wg] = static_cast<uint8_t>(ebits);  // 0 for rows past valid
+        }
+        sync_lds();
+        if (tid < kBM) {
+          const int q = tid;
+          const int rr = (q & ~63) + (q & 15), ks = (q >> 4) & 3;
+          uint32_t w = 0;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) w |= static_cast<uint32_t>(ex[(rr + 16 * g) * 4 + ks]) << (8 * g);
-            reinterpret_cast<uint32_t*>(p.c_scale)[static_cast<int64_t>(nt) * p.cs_rs + static_cast<int64_t>(mnat) * kBM + q] = w;
-          }
-        } else {
-          // 1x128 group = the row's 128 columns of this tile
-          m = fmaxf(m, __shfl_xor(m, 1, 64));
-          if (r < valid) {
-            const float s = scale_from_amax(m);
-            const float inv = 1.0f / s;
-            uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out + nt * 128 + half * 64;
+          for (int gq = 0; gq < 4; ++gq) w |= static_cast<uint32_t>(ex[(rr + 16 * gq) * 4 + ks]) << (8 * gq);
+          reinterpret_cast<uint32_t*>(p.c_scale)[static_cast<int64_t>(nt) * p.cs_rs +
+                                                 static_cast<int64_t>(cur.mnat) * kBM + q] = w;
+        }
+      } else {
+        // 1x128 group = the row's 128 columns of this tile, spread over the 4
+        // waves of the group.  h (rounded to bf16) replaces the gate half of the
+        // accumulators; each wave's row maxima go through LDS; the quantised
+        // tile (256 rows x 128 bytes = 8 chunks) is staged in ct.
+        float* rmax = reinterpret_cast<float*>(smem + kEpiOff);  // [256 rows][4 waves]
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              uint32_t qw[4];
+        for (int i = 0; i < 8; ++i) {
+          if (i < live_sub) {
+            float m = 0.0f;
 #pragma unroll
-              for (int h2 = 0; h2 < 2; ++h2) {
-                const uint4 v = *reinterpret_cast<const uint4*>(src + u * 16 + h2 * 8);
-                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                  const uint32_t lo = w[2 * q], hi = w[2 * q + 1];
-                  qw[h2 * 2 + q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(lo & 0xffffu), s, inv),
-                                               quot_e4m3(bf16_bits_to_f32(lo >> 16), s, inv),
-                                               quot_e4m3(bf16_bits_to_f32(hi & 0xffffu), s, inv),
-                                               quot_e4m3(bf16_bits_to_f32(hi >> 16), s, inv));
-                }
-              }
-              *reinterpret_cast<uint4*>(dst + u * 16) = uint4{qw[0], qw[1], qw[2], qw[3]};
+            for (int j = 0; j < 2; ++j) {
+              const uint2 v = h_of(i, j);
+              m = fmaxf(m, absmax(v));
+              acc[i][j][0] = bf16_bits_to_f32(v.x & 0xffffu);
+              acc[i][j][1] = bf16_bits_to_f32(v.x >> 16);
+              acc[i][j][2] = bf16_bits_to_f32(v.y & 0xffffu);
+              acc[i][j][3] = bf16_bits_to_f32(v.y >> 16);
             }
-            if (half == 0) p.c_scale[static_cast<int64_t>(nt) * p.rows + row0 + r] = s;
+            m = wave_row_max(m);
+            if (elg == 0) rmax[(wave_row0 + i * 16 + el16) * 4 + wg] = m;
           }
         }
+        sync_lds();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = wave_row0 + i * 16 + el16;
+          if (i < live_sub) {
+            const f32x4 mm = *reinterpret_cast<const f32x4*>(rmax + r * 4);
+            const float s = scale_from_amax(fmaxf(fmaxf(mm.x, mm.y), fmaxf(mm.z, mm.w)));
+            const float inv = 1.0f / s;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const int c = wg * 2 + j;
+              *reinterpret_cast<uint32_t*>(ct + r * 128 + ((c ^ (r & 7)) << 4) + elg * 4) =
+                  pack_e4m3x4(quot_e4m3(acc[i][j][0], s, inv), quot_e4m3(acc[i][j][1], s, inv),
+                              quot_e4m3(acc[i][j][2], s, inv), quot_e4m3(acc[i][j][3], s, inv));
+            }
+            if (wg == 0 && elg == 0 && r < valid) p.c_scale[static_cast<int64_t>(nt) * p.rows + row0 + r] = s;
+          }
+        }
+        sync_lds();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int idx = wave * 64 + eln + kThreads * u, r = idx >> 3, c = idx & 7;
+          if (r < valid) {
+            const uint4 v = *reinterpret_cast<const uint4*>(ct + r * 128 + ((c ^ (r & 7)) << 4));
+            *reinterpret_cast<uint4*>(static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out +
+                                      nt * 128 + c * 16) = v;
+          }
+        }
+        sync_lds();  // ct is the next tile's A(1) stage
       }
     }
+
+    if (nxt.t < 0) break;
+    if (!pipe) start_tile(nxt, buf ^ 1, gstep + k_steps);
+    cur = nxt;
+    buf ^= 1;
+    gstep += k_steps;
   }
 }
+#undef HK_SLOT
+#undef HK_CAP
+#undef HK_SET_B
+#undef HK_NROW
+#undef HK_BS
+#pragma clang diagnostic pop
 
 // Packed weight layout (a load-time transform; the grouped GEMMs then stream
 // every weight panel sequentially instead of 128 bytes from each of 256 rows
