@@ -77,6 +77,9 @@ def parse():
                          "so that no launch finds its operands in L2/MALL (0: one copy)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (counter calibration)")
+    ap.add_argument("--summarize-counters", metavar="DIR", default=None,
+                    help="no GPU work: turn the rocprofv3 --pmc output under DIR (mfma/, lds/) of this config "
+                         "into profiles/*_counters.md")
     ap.add_argument("--summarize-profile", metavar="DIR", default=None,
                     help="no GPU work: turn the rocprofv3 output under DIR (trace/, FETCH_SIZE/, "
                          "WRITE_SIZE/) of this config into profiles/*.md and profiles/traffic.json")
@@ -649,6 +652,79 @@ def summarize_profile(args):
                       "traffic": traffic}))
 
 
+# Counter passes (one rocprofv3 run each; every pass stays within one run's
+# hardware counter limits).  MfmaUtil = MFMA-busy cycles of all SIMDs / (GPU
+# active cycles x SIMDs); LDSBankConflict = LDS bank-conflict stall cycles as a
+# share of GPU time; LdsBankConflict = conflict cycles per conflict-free LDS cycle.
+PMC_PASSES = {
+    "mfma": "MfmaUtil VALUBusy SQ_VALU_MFMA_COEXEC_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F8 "
+            "SQ_BUSY_CYCLES",
+    "lds": "LDSBankConflict LdsBankConflict SQ_INSTS_LDS SQ_WAIT_INST_LDS SQ_LDS_IDX_ACTIVE",
+}
+PROF_PMC_PASS_CMD = ("rocprofv3 --pmc {ctrs} --output-format csv -d {d}/{p} -o run -- "
+                     "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu")
+
+
+def summarize_counters(args):
+    """profiles/<workload>_counters.md from the two counter passes under DIR:
+    per kernel, the average over its dispatches of each metric."""
+    import csv
+    import collections
+    dense = args.config in DENSE
+    cfg = DENSE[args.config] if dense else CONFIGS[args.config]
+    d = args.summarize_counters
+    vals = collections.defaultdict(lambda: collections.defaultdict(list))
+    for p in PMC_PASSES:
+        path = os.path.join(d, p, "run_counter_collection.csv")
+        per = collections.defaultdict(lambda: collections.defaultdict(float))
+        names = {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                lab = _kernel_label(r["Kernel_Name"], dense)
+                if lab is None:
+                    continue
+                per[(lab, r["Dispatch_Id"])][r["Counter_Name"]] += float(r["Counter_Value"])
+                names[r["Counter_Name"]] = 1
+        for (lab, _), ctrs in per.items():
+            for c, v in ctrs.items():
+                vals[lab][c].append(v)
+    avg = {lab: {c: sum(v) / len(v) for c, v in cs.items()} for lab, cs in vals.items()}
+    ndisp = {lab: max(len(v) for v in cs.values()) for lab, cs in vals.items()}
+    name = f"gemm_{args.config}" if dense else f"moe_layer_{args.config}"
+    out = os.path.join(ROOT, "profiles", f"{name}_counters.md")
+    with open(out, "w") as f:
+        f.write(f"# rocprofv3 counters: {'dense GEMM' if dense else 'MoE layer'}, workload `{args.config}`\n\n")
+        f.write(f"Config: {json.dumps(cfg)}\n\n")
+        f.write("Two counter passes, one rocprofv3 run each (repo root):\n\n")
+        for p, ctrs in PMC_PASSES.items():
+            f.write("    " + PROF_PMC_PASS_CMD.format(ctrs=ctrs, d="<out>", p=p, c=args.config) + "\n")
+        f.write("\nCounter collection serialises the dispatches, so every kernel runs alone on the GPU "
+                "here (the narrow kernels do not overlap the 256x256 GEMMs as they do in the timed layer). "
+                "MfmaUtil is MFMA-busy cycles summed over all 1024 SIMDs / (GPU-active cycles x 1024); a "
+                "kernel that leaves CUs idle (the first 256x256 GEMM yields 64 CUs to the narrow kernel while "
+                "narrow experts exist) is charged for them.  MFMA FLOPs = SQ_INSTS_VALU_MFMA_MOPS_F8 x 512, "
+                "the FLOPs the matrix cores executed (padded rows of partial tiles included).  "
+                "LDSBankConflict: bank-conflict stall cycles as % of GPU time per CU; LdsBankConflict: "
+                "conflict cycles per conflict-free LDS cycle.\n\n")
+        f.write("| kernel | dispatches | MfmaUtil % | VALUBusy % | MFMA-VALU co-exec / MFMA busy | MFMA TFLOP per "
+                "dispatch | LDSBankConflict % | LdsBankConflict | LDS instr. per dispatch |\n"
+                "|---|---|---|---|---|---|---|---|---|\n")
+        for lab in sorted(avg, key=lambda x: -avg[x].get("SQ_VALU_MFMA_BUSY_CYCLES", 0)):
+            a = avg[lab]
+            busy = a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+            co = a.get("SQ_VALU_MFMA_COEXEC_CYCLES", 0.0)
+
+            def g(k, fmt):
+                return fmt.format(a[k]) if k in a else "-"
+            f.write(f"| {lab} | {ndisp[lab]} | {g('MfmaUtil', '{:.1f}')} | {g('VALUBusy', '{:.1f}')} | "
+                    + (f"{co / busy:.2f}" if busy > 0 else "-") + " | "
+                    + (f"{a['SQ_INSTS_VALU_MFMA_MOPS_F8'] * 512 / 1e12:.3f}" if "SQ_INSTS_VALU_MFMA_MOPS_F8" in a
+                       else "-")
+                    + f" | {g('LDSBankConflict', '{:.2f}')} | {g('LdsBankConflict', '{:.4f}')} | "
+                    + f"{g('SQ_INSTS_LDS', '{:,.0f}')} |\n")
+    print(json.dumps({"written": [os.path.relpath(out, ROOT)]}))
+
+
 def dense_cpu_baseline(a_q, sa, b_q, sb, cfg, budget_s):
     """The path's PyTorch CPU version of the dense GEMM: dequantise A and B to
     fp32 (per-tensor scales, or 1x32 e8m0 for the MX shape), one fp32
@@ -760,6 +836,9 @@ def main():
     args = parse()
     if args.summarize_profile:
         summarize_profile(args)
+        return
+    if args.summarize_counters:
+        summarize_counters(args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: run with --gpus 1 "
