@@ -20,7 +20,6 @@ namespace hkmoe {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define HK_LDS __attribute__((address_space(3)))
 
@@ -73,13 +72,6 @@ __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ f32x4 mfma_e4m3_16x16x128(const i32x8& a, const i32x8& b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
-
-// D(32x32 fp32) += A(32x64 e4m3) . B(32x64 e4m3)^T: lane l supplies row l % 32
-// and 32 bytes of K (group l / 32) of each operand; output lane l, register
-// r holds D[8*(r/4) + 4*(l/32) + r%4][l % 32].
-__device__ __forceinline__ f32x16 mfma_e4m3_32x32x64(const i32x8& a, const i32x8& b, f32x16 c) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------
