@@ -498,6 +498,8 @@ def _kernel_label(name, dense=False):
     if "gemm_fp8_narrow" in name:
         epi = name.split("Epi)")[1][0] if "Epi)" in name else "?"
         return "narrow_gemm1" if epi == "3" else "narrow_gemm2"
+    if "gemm_fp8_small" in name:  # the dense GEMM's 128x128-tile kernel
+        return "gemm"
     n = name[len("void "):] if name.startswith("void ") else name  # template kernels
     if n.startswith("hkmoe::"):
         return n[len("hkmoe::"):].split("(")[0].split("<")[0].replace("_kernel", "")
@@ -789,10 +791,33 @@ def dense_main(args):
         step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # Eager launches from Python: for a kernel of tens of microseconds the host
+    # issue rate, not the GPU, sets this time; reported beside the value.
     t0 = time.perf_counter()
     e0.record()
     for _ in range(args.steps):
         step()
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    # The timed steps: the same launches, captured once into a HIP graph and
+    # replayed, so they run back to back on the GPU (the wall time of one replay
+    # of `steps` launches, synchronised on both sides).
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(args.steps):
+            step()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    graph.replay()
     e1.record()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
@@ -820,7 +845,8 @@ def dense_main(args):
         "data": "synthetic (seeded torch normal on device, quantised by the path's quantisers)",
         "config": {"workload": f"{args.config}_gemm", "M": M, "N": N, "K": K,
                    "scales": "1x32 e8m0 (MX)" if cfg["mx"] else "per-tensor", "out": cfg["out"],
-                   "operand_copies": n_rot},
+                   "operand_copies": n_rot, "launch": "graph"},
+        "eager_ms_per_step": round(eager_ms, 4),
         "pct_fp8_peak": round(100.0 * value / PEAK_FP8_TFLOPS, 2),
         "roofline": {"bound": "mfma", "kernel": "gemm_mx" if cfg["mx"] else "gemm_fp8",
                      "achieved": round(ach, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",

@@ -16,6 +16,7 @@
 #include "../../include/hkmoe.h"
 #include "gemm_fp8.hpp"
 #include "gemm_narrow.hpp"
+#include "gemm_small.hpp"
 #include "moe_kernels.hpp"
 
 #include <cstdlib>
@@ -96,6 +97,25 @@ int launch_gemm(GemmParams p, hipStream_t stream, int grid_override = 0) {
   const int grid = grid_override > 0 ? grid_override : device_cus();
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), kLdsBytes, stream, p);
   return check_launch("gemm_fp8_persistent");
+}
+
+// The dense GEMM on 128x128 tiles (gemm_small.hpp): one workgroup per tile,
+// the grid a whole number of 4x8 tile blocks.
+template <bool F32OUT>
+int launch_gemm_small(const SmallGemmParams& p, hipStream_t stream) {
+  static bool attr_set[kMaxDevices] = {false};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  auto kern = gemm_fp8_small<F32OUT>;
+  if (dev >= 0 && dev < kMaxDevices && !attr_set[dev]) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, kSmLdsBytes);
+    if (err != hipSuccess) return fail(HKMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(err));
+    attr_set[dev] = true;
+  }
+  const int grid = ((p.m_tiles + 3) / 4) * p.nbn * 32;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kSmThreads), kSmLdsBytes, stream, p);
+  return check_launch("gemm_fp8_small");
 }
 
 // Prefetch depth of the narrow kernel for K / 128 steps: the largest of 8, 4,
@@ -304,6 +324,25 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
              "gemm_fp8: operand too large for 32-bit buffer offsets");
   HK_REQUIRE(out_dtype == HKMOE_BF16 || out_dtype == HKMOE_F32, "gemm_fp8: bad out_dtype %d", out_dtype);
   if (m == 0) return HKMOE_OK;
+  auto s = static_cast<hipStream_t>(stream);
+  // Fewer 256x256 tiles than two per CU: 128x128 tiles, one workgroup each.
+  if (((m + kBM - 1) / kBM) * (n / kBN) < 2ll * device_cus()) {
+    SmallGemmParams q{};
+    q.a = static_cast<const uint8_t*>(a);
+    q.b = static_cast<const uint8_t*>(b);
+    q.c = c;
+    q.a_scale = scale_a;
+    q.b_scale = scale_b;
+    q.m = static_cast<int32_t>(m);
+    q.n = static_cast<int32_t>(n);
+    q.k = static_cast<int32_t>(k);
+    q.a_bytes = static_cast<uint32_t>(std::min<int64_t>(m * k, 0xffffffffll));
+    q.b_bytes = static_cast<uint32_t>(std::min<int64_t>(n * k, 0xffffffffll));
+    q.m_tiles = static_cast<int32_t>((m + kSmTile - 1) / kSmTile);
+    q.n_tiles = static_cast<int32_t>(n / kSmTile);
+    q.nbn = (q.n_tiles + 7) / 8;
+    return out_dtype == HKMOE_BF16 ? launch_gemm_small<false>(q, s) : launch_gemm_small<true>(q, s);
+  }
   GemmParams p{};
   p.a = static_cast<const uint8_t*>(a);
   p.b = static_cast<const uint8_t*>(b);
@@ -318,7 +357,6 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
   p.n_out = static_cast<int32_t>(n);
   p.n_tiles = static_cast<int32_t>(n / kBN);
   p.blk_m_log2 = 2;  // 4 x 8 tile blocks
-  auto s = static_cast<hipStream_t>(stream);
   return out_dtype == HKMOE_BF16 ? launch_gemm<Epi::kStoreBf16, Scale::kTensor>(p, s)
                                  : launch_gemm<Epi::kStoreF32, Scale::kTensor>(p, s);
 }
