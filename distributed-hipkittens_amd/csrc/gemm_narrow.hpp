@@ -145,20 +145,11 @@ __device__ __forceinline__ void lds_write_b64(uint32_t a, uint2 v) {
   asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(v) : "memory");
 }
 
-// 64 bf16 (128 bytes) at a, complete on return
-__device__ __forceinline__ void lds_read_128B(uint32_t a, uint4 (&v)[8]) {
-  asm volatile(
-      "ds_read_b128 %0, %8\n\t"
-      "ds_read_b128 %1, %8 offset:16\n\t"
-      "ds_read_b128 %2, %8 offset:32\n\t"
-      "ds_read_b128 %3, %8 offset:48\n\t"
-      "ds_read_b128 %4, %8 offset:64\n\t"
-      "ds_read_b128 %5, %8 offset:80\n\t"
-      "ds_read_b128 %6, %8 offset:96\n\t"
-      "ds_read_b128 %7, %8 offset:112\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
-      : "v"(a));
+// 16 bytes at a, complete on return
+__device__ __forceinline__ uint4 lds_read_u4(uint32_t a) {
+  uint4 v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
+  return v;
 }
 
 // LDS writes done, then the workgroup barrier (no vmcnt: DMA stays in flight)
@@ -489,46 +480,36 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
         lds_write_b64(lds_addr(ct + (16 * i + l16) * kNarrowCtLd + 16 * wave + 4 * lg), v);
       }
       lds_barrier();
-      if (tid < 2 * kNarrowRows) {
-        const int r = tid >> 1, half = tid & 1;
-        uint4 hrow[8];
-        lds_read_128B(lds_addr(ct + r * kNarrowCtLd + half * 64), hrow);
+      // The valid rows' 128 columns (one 1x128 group each) requantised to
+      // e4m3: 16 lanes per row, 8 columns each, the row maximum by shuffles
+      // within the 16 lanes; a 10-row segment keeps 160 lanes busy instead of 20.
+      for (int base = 0; base < 16 * C.valid; base += kThreads) {
+        const int idx = base + tid, r = idx >> 4, q = idx & 15;
+        const bool live = r < C.valid;
+        uint4 hv = uint4{0u, 0u, 0u, 0u};
+        if (live) hv = lds_read_u4(lds_addr(ct + r * kNarrowCtLd + q * 8));
+        const uint32_t w[4] = {hv.x, hv.y, hv.z, hv.w};
         float m = 0.0f;
-        if (r < C.valid) {
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const uint4 v = hrow[u];
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        for (int u = 0; u < 4; ++u)
+          m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(w[u] & 0xffffu)), fabsf(bf16_bits_to_f32(w[u] >> 16))));
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(w[q] & 0xffffu)), fabsf(bf16_bits_to_f32(w[q] >> 16))));
-          }
-        }
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        if (r < C.valid) {
+        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (live) {
           const float sc = scale_from_amax(m);
           const float inv = 1.0f / sc;
-          uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(C.row0 + r) * p.n_out +
-                         C.nt * 128 + half * 64;
+          uint32_t qw[2];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            uint32_t qw[4];
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-              const uint4 v = hrow[2 * u + h2];
-              const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-              for (int q = 0; q < 2; ++q) {
-                const uint32_t lo = w[2 * q], hi = w[2 * q + 1];
-                qw[h2 * 2 + q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(lo & 0xffffu), sc, inv),
-                                             quot_e4m3(bf16_bits_to_f32(lo >> 16), sc, inv),
-                                             quot_e4m3(bf16_bits_to_f32(hi & 0xffffu), sc, inv),
-                                             quot_e4m3(bf16_bits_to_f32(hi >> 16), sc, inv));
-              }
-            }
-            *reinterpret_cast<uint4*>(dst + u * 16) = uint4{qw[0], qw[1], qw[2], qw[3]};
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const uint32_t lo = w[2 * h2], hi = w[2 * h2 + 1];
+            qw[h2] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(lo & 0xffffu), sc, inv),
+                                 quot_e4m3(bf16_bits_to_f32(lo >> 16), sc, inv),
+                                 quot_e4m3(bf16_bits_to_f32(hi & 0xffffu), sc, inv),
+                                 quot_e4m3(bf16_bits_to_f32(hi >> 16), sc, inv));
           }
-          if (half == 0) p.c_scale[static_cast<int64_t>(C.nt) * p.rows + C.row0 + r] = sc;
+          uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(C.row0 + r) * p.n_out + C.nt * 128 + q * 8;
+          *reinterpret_cast<uint2*>(dst) = uint2{qw[0], qw[1]};
+          if (q == 0) p.c_scale[static_cast<int64_t>(C.nt) * p.rows + C.row0 + r] = sc;
         }
       }
       // the staging tile is next written after at least P more barriers
