@@ -323,8 +323,7 @@ __global__ __launch_bounds__(256) void requant_group_kernel(const uint16_t* __re
     const float a = bf16_bits_to_f32(pair & 0xffffu), b = bf16_bits_to_f32(pair >> 16);
     const float amax = wave_max(fmaxf(fabsf(a), fabsf(b)));
     const float s = scale_from_amax(amax);
-    const float inv = 1.0f / s;
-    const uint32_t q = pack_e4m3x4(quot_e4m3(a, s, inv), quot_e4m3(b, s, inv), 0.0f, 0.0f) & 0xffffu;
+    const uint32_t q = pack_e4m3x4(quot_e4m3(a, s), quot_e4m3(b, s), 0.0f, 0.0f) & 0xffffu;
     *reinterpret_cast<uint16_t*>(hq + base) = static_cast<uint16_t>(q);
     if (lane == 0) hs_t[static_cast<int64_t>(g) * rows + r] = s;
   }
@@ -336,7 +335,6 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
                                                              uint8_t* __restrict__ hq,
                                                              float* __restrict__ hs) {
   const float s = scale_from_amax(*amax);
-  const float inv = 1.0f / s;
   if (blockIdx.x == 0 && threadIdx.x == 0) hs[0] = s;
   for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n8; i += static_cast<int64_t>(gridDim.x) * 256) {
     const uint4 v = reinterpret_cast<const uint4*>(h)[i];
@@ -346,10 +344,10 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const uint32_t p0 = w[q * 2], p1 = w[q * 2 + 1];
-      op[q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(p0 & 0xffffu), s, inv),
-                          quot_e4m3(bf16_bits_to_f32(p0 >> 16), s, inv),
-                          quot_e4m3(bf16_bits_to_f32(p1 & 0xffffu), s, inv),
-                          quot_e4m3(bf16_bits_to_f32(p1 >> 16), s, inv));
+      op[q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(p0 & 0xffffu), s),
+                          quot_e4m3(bf16_bits_to_f32(p0 >> 16), s),
+                          quot_e4m3(bf16_bits_to_f32(p1 & 0xffffu), s),
+                          quot_e4m3(bf16_bits_to_f32(p1 >> 16), s));
     }
     reinterpret_cast<uint2*>(hq)[i] = o;
   }
