@@ -75,12 +75,6 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 int route_blocks(int64_t t) { return static_cast<int>((t + kRouteTok - 1) / kRouteTok); }
 
-int pow2_at_least(int v) {
-  int p = 1;
-  while (p < v) p <<= 1;
-  return p;
-}
-
 template <Epi EPI, Scale SC>
 int launch_gemm(GemmParams p, hipStream_t stream, int grid_override = 0) {
   p.a_bytes = static_cast<uint32_t>(std::min<int64_t>(p.a_rows * p.K, 0xffffffffll));
@@ -274,11 +268,11 @@ int launch_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32
                           int32_t* tile_counters, int narrow_max, int32_t* narrow_info,
                           hipStream_t stream) {
   const int nblk = route_blocks(num_tokens);
-  const int e_stride = pow2_at_least(num_experts);
-  const int parts = kScanThreads / e_stride;
-  hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(kScanThreads), 0, stream, block_counts, nblk,
-                     num_experts, e_stride, parts, counts, offsets, block_base, mtile_offsets,
-                     mtile_list, kBM, amax_reset, tile_counters, narrow_max, narrow_info);
+  hipLaunchKernelGGL(expert_block_scan_kernel, dim3((num_experts + kOffExperts - 1) / kOffExperts),
+                     dim3(kScanThreads), 0, stream, block_counts, nblk, num_experts, counts, block_base);
+  HK_TRY(check_launch("expert_block_scan_kernel"));
+  hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(kScanThreads), 0, stream, num_experts, counts, offsets,
+                     mtile_offsets, mtile_list, kBM, amax_reset, tile_counters, narrow_max, narrow_info);
   return check_launch("expert_offsets_kernel");
 }
 
@@ -373,10 +367,11 @@ int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_expert
   HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK,
              "route_topk: top_k=%d outside [1, min(E, %d)]", top_k, kMaxTopK);
   if (num_tokens == 0) return HKMOE_OK;
-  const int chunks = (num_experts + 63) / 64;
-  auto kern = chunks <= 1 ? route_topk_kernel<1> : chunks <= 2 ? route_topk_kernel<2>
-            : chunks <= 4 ? route_topk_kernel<4> : chunks <= 8 ? route_topk_kernel<8>
-                          : route_topk_kernel<16>;
+  const int per_lane = (num_experts + 15) / 16;  // experts per lane of a token's 16-lane row
+  auto kern = per_lane <= 1 ? route_topk_kernel<1> : per_lane <= 2 ? route_topk_kernel<2>
+            : per_lane <= 4 ? route_topk_kernel<4> : per_lane <= 8 ? route_topk_kernel<8>
+            : per_lane <= 16 ? route_topk_kernel<16> : per_lane <= 32 ? route_topk_kernel<32>
+                             : route_topk_kernel<64>;
   hipLaunchKernelGGL(kern, dim3(route_blocks(num_tokens)), dim3(kTopkThreads), 0,
                      static_cast<hipStream_t>(stream), logits, static_cast<int>(num_tokens),
                      num_experts, top_k, topk_idx, topk_w, block_counts);

@@ -14,7 +14,7 @@ namespace hkmoe {
 
 constexpr int kRouteTok = 32;      // tokens per routing/scatter workgroup
 constexpr int kRouteThreads = 256; // scatter: 4 waves per 32-token block
-constexpr int kTopkThreads = 1024; // top-k: 16 waves, 2 tokens each
+constexpr int kTopkThreads = 512;  // top-k: 8 waves, 4 tokens each (16 lanes per token)
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kScanThreads = 1024;
@@ -28,62 +28,87 @@ __device__ __forceinline__ bool route_better(float av, int ai, float bv, int bi)
   return av > bv || (av == bv && ai < bi);
 }
 
+// One level of a row argmax: every lane takes the better of its own entry and
+// the one that DPP control CTRL (a permutation within rows of 16 lanes) brings.
+template <int CTRL>
+__device__ __forceinline__ void route_best_dpp(float& bv, int& bi) {
+  const float ov =
+      __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(bv), __float_as_int(bv), CTRL, 0xf, 0xf, false));
+  const int oi = __builtin_amdgcn_update_dpp(bi, bi, CTRL, 0xf, 0xf, false);
+  if (route_better(ov, oi, bv, bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
 // ---------------------------------------------------------------------------
-// 1. top-k + softmax + per-block histogram.  One wave per token; CH = number
-//    of 64-expert chunks a lane holds (power of two >= ceil(E / 64)).
+// 1. top-k + softmax + per-block histogram.  16 lanes (one row of the wave) per
+//    token, 4 tokens per wave; lane s of a token's row holds experts c*16 + s,
+//    c < CH (CH: power of two >= ceil(E / 16)).  Each of the k rounds takes
+//    the lane's best untaken expert and reduces the row by DPP swaps (quad
+//    pairs, quad swap, half-row and row mirrors): VALU only, and a round's
+//    work is shared by four tokens.  route_better is a total order, so the
+//    reduction order does not change the winner.
 // ---------------------------------------------------------------------------
 template <int CH>
 __global__ __launch_bounds__(kTopkThreads) void route_topk_kernel(
     const float* __restrict__ logits, int num_tokens, int num_experts, int top_k,
     int32_t* __restrict__ topk_idx, float* __restrict__ topk_w, int32_t* __restrict__ block_counts) {
+  static_assert(kTopkThreads == 16 * kRouteTok, "one 16-lane row per token");
+  static_assert(CH <= 64, "taken mask");
   __shared__ int hist[kMaxExperts];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int sub = threadIdx.x & 15;
   for (int e = threadIdx.x; e < num_experts; e += kTopkThreads) hist[e] = 0;
   __syncthreads();
 
-  const int t0 = blockIdx.x * kRouteTok;
-  for (int tt = wave; tt < kRouteTok; tt += kTopkThreads / 64) {
-    const int t = t0 + tt;
-    if (t >= num_tokens) break;
+  const int t = blockIdx.x * kRouteTok + (threadIdx.x >> 4);
+  if (t < num_tokens) {  // uniform over the token's row
     const float* row = logits + static_cast<int64_t>(t) * num_experts;
     float v[CH];
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int id = c * 64 + lane;
+      const int id = c * 16 + sub;
       v[c] = (id < num_experts) ? row[id] : 0.0f;
     }
-    uint32_t taken = 0;
-    float my_v = 0.0f, v0 = 0.0f;
-    int my_id = 0;
+    uint64_t taken = 0;
+    float v0 = 0.0f, mv0 = 0.0f, mv1 = 0.0f;  // winners j (lane j % 16): j < 16 in mv0, else mv1
+    int mi0 = 0, mi1 = 0;
     for (int j = 0; j < top_k; ++j) {
       float bv = 0.0f;
       int bi = -1;
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        const int id = c * 64 + lane;
+        const int id = c * 16 + sub;
         if (id < num_experts && !((taken >> c) & 1u) && route_better(v[c], id, bv, bi)) {
           bv = v[c];
           bi = id;
         }
       }
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (route_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-      }
-      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+      route_best_dpp<0xB1>(bv, bi);   // quad_perm [1,0,3,2]
+      route_best_dpp<0x4E>(bv, bi);   // quad_perm [2,3,0,1]
+      route_best_dpp<0x141>(bv, bi);  // row_half_mirror
+      route_best_dpp<0x140>(bv, bi);  // row_mirror
+      if ((bi & 15) == sub) taken |= uint64_t{1} << (bi >> 4);
       if (j == 0) v0 = bv;
-      if (lane == j) { my_v = bv; my_id = bi; }
+      if ((j & 15) == sub) {
+        if (j < 16) { mv0 = bv; mi0 = bi; } else { mv1 = bv; mi1 = bi; }
+      }
     }
-    const float ex = (lane < top_k) ? expf(my_v - v0) : 0.0f;
+    // softmax over the winners: exp(v_j - v_0) / sum_j exp(v_j - v_0), the sum
+    // taken in j order
+    const float ex0 = (sub < top_k) ? expf(mv0 - v0) : 0.0f;
+    const float ex1 = (sub + 16 < top_k) ? expf(mv1 - v0) : 0.0f;
     float tot = 0.0f;
-    for (int j = 0; j < top_k; ++j) tot = tot + __shfl(ex, j, 64);
-    if (lane < top_k) {
-      topk_idx[static_cast<int64_t>(t) * top_k + lane] = my_id;
-      topk_w[static_cast<int64_t>(t) * top_k + lane] = ex / tot;
-      atomicAdd(&hist[my_id], 1);
+    for (int j = 0; j < top_k; ++j) tot = tot + __shfl(j < 16 ? ex0 : ex1, j & 15, 16);
+    if (sub < top_k) {
+      topk_idx[static_cast<int64_t>(t) * top_k + sub] = mi0;
+      topk_w[static_cast<int64_t>(t) * top_k + sub] = ex0 / tot;
+      atomicAdd(&hist[mi0], 1);
+    }
+    if (sub + 16 < top_k) {
+      topk_idx[static_cast<int64_t>(t) * top_k + sub + 16] = mi1;
+      topk_w[static_cast<int64_t>(t) * top_k + sub + 16] = ex1 / tot;
+      atomicAdd(&hist[mi1], 1);
     }
   }
   __syncthreads();
@@ -92,52 +117,41 @@ __global__ __launch_bounds__(kTopkThreads) void route_topk_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// 2. offsets: per-expert exclusive scan over blocks, then over experts.
-//    One workgroup of 1024 threads; thread = (part, expert).
+// 2. offsets, in two launches.
+//  a. expert_block_scan: per expert, the exclusive prefix of its counts over
+//     the routing blocks (block_base) and its total (counts).  kOffExperts
+//     experts per workgroup, each over kOffParts ranges of blocks, so the
+//     block counts are read by many CUs at once (a single workgroup spent
+//     most of its time waiting for them).
+//  b. expert_offsets: one workgroup of 1024 threads, thread = expert: scans
+//     over experts (offsets, M-tile offsets), the M-tile list, counters.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int incl = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int n = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += n;
-  }
-  if (lane == 63) wave_tot[wave] = incl;
-  __syncthreads();
-  if (wave == 0) {
-    const int nw = blockDim.x >> 6;
-    int wv = lane < nw ? wave_tot[lane] : 0;
-    int wi = wv;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int n = __shfl_up(wi, o, 64);
-      if (lane >= o) wi += n;
-    }
-    if (lane < nw) wave_tot[lane] = wi - wv;
-  }
-  __syncthreads();
-  const int r = wave_tot[wave] + incl - v;
-  __syncthreads();
-  return r;
-}
+constexpr int kOffExperts = 16;                        // experts per block-scan workgroup
+constexpr int kOffParts = kScanThreads / kOffExperts;  // block ranges per expert
+constexpr int kOffCache = 32;                          // counts a thread keeps in registers
 
-__global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
-    const int32_t* __restrict__ block_counts, int nblk, int num_experts, int e_stride, int parts,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ block_base,
-    int32_t* __restrict__ mtile_offsets, int32_t* __restrict__ mtile_list, int tile_m,
-    float* amax_reset, int32_t* tile_counters, int narrow_max, int32_t* narrow_info) {
-  __shared__ int part_sum[kScanThreads];
-  __shared__ int wave_tot[kScanThreads / 64];
+__global__ __launch_bounds__(kScanThreads) void expert_block_scan_kernel(
+    const int32_t* __restrict__ block_counts, int nblk, int num_experts, int32_t* __restrict__ counts,
+    int32_t* __restrict__ block_base) {
+  __shared__ int part_sum[kOffParts][kOffExperts];
   const int tid = threadIdx.x;
-  const int e = tid % e_stride;
-  const int part = tid / e_stride;
-  const int per = (nblk + parts - 1) / parts;
-  const int b0 = part * per, b1 = min(nblk, b0 + per);
-  const bool act = (e < num_experts) && (part < parts);
-
+  const int el = tid % kOffExperts, part = tid / kOffExperts;
+  const int e = blockIdx.x * kOffExperts + el;
+  const int per = (nblk + kOffParts - 1) / kOffParts;
+  const int b0 = min(nblk, part * per), b1 = min(nblk, b0 + per);
+  const bool act = e < num_experts;
+  // up to kOffCache counts are loaded at once and kept for the block_base
+  // pass; longer ranges are read twice, 16 loads in flight at a time
+  const bool cached = per <= kOffCache;
+  int cache[kOffCache];
   int s = 0;
-  if (act) {
+  if (act && cached) {
+#pragma unroll
+    for (int u = 0; u < kOffCache; ++u)
+      cache[u] = (b0 + u < b1) ? block_counts[static_cast<int64_t>(b0 + u) * num_experts + e] : 0;
+#pragma unroll
+    for (int u = 0; u < kOffCache; ++u) s += cache[u];
+  } else if (act) {
     for (int b = b0; b < b1; b += 16) {
       int c[16];
 #pragma unroll
@@ -147,20 +161,25 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
       for (int u = 0; u < 16; ++u) s += c[u];
     }
   }
-  part_sum[tid] = act ? s : 0;
+  part_sum[part][el] = s;
   __syncthreads();
-  // prefix over parts for this expert, and the expert total
+  if (!act) return;
+  // prefix over the ranges before this one, and the expert's total
   int before = 0, total = 0;
-  if (e < num_experts) {
-    for (int q = 0; q < parts; ++q) {
-      const int v = part_sum[q * e_stride + e];
-      if (q < part) before += v;
-      total += v;
-    }
+  for (int q = 0; q < kOffParts; ++q) {
+    const int v = part_sum[q][el];
+    if (q < part) before += v;
+    total += v;
   }
-  if (act) {
-    // 16 independent loads in flight, then the running sum and the stores
-    int run = before;
+  if (part == 0) counts[e] = total;
+  int run = before;
+  if (cached) {
+#pragma unroll
+    for (int u = 0; u < kOffCache; ++u) {
+      if (b0 + u < b1) block_base[static_cast<int64_t>(b0 + u) * num_experts + e] = run;
+      run += cache[u];
+    }
+  } else {
     for (int b = b0; b < b1; b += 16) {
       int c[16];
 #pragma unroll
@@ -173,46 +192,89 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
       }
     }
   }
-  // scan over experts (threads with part == 0 carry the expert totals)
-  const int cnt = (part == 0 && e < num_experts) ? total : 0;
-  const int mt = (cnt + tile_m - 1) / tile_m;
-  const int off = block_exclusive_scan(cnt, wave_tot);
-  const int moff = block_exclusive_scan(mt, wave_tot);
-  if (part == 0 && e < num_experts) {
-    counts[e] = cnt;
-    offsets[e] = off;
-    mtile_offsets[e] = moff;
-    if (e == num_experts - 1) {
-      offsets[num_experts] = off + cnt;
-      mtile_offsets[num_experts] = moff + mt;
+}
+
+// Exclusive scans of N values per thread over the workgroup, all in one pass.
+template <int N>
+__device__ __forceinline__ void block_exclusive_scan_n(int (&v)[N], int (*wave_tot)[N]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) incl[i] = v[i];
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int n = __shfl_up(incl[i], o, 64);
+      if (lane >= o) incl[i] += n;
     }
   }
-  if (mtile_list != nullptr) {
-    // M-tile list [(expert, first row)]: first the experts with at least one
-    // full tile, each with all its tiles (full ones, then its partial one),
-    // in expert order; then the single partial tiles of the smaller experts;
-    // last, with narrow_max > 0, the experts of 1..narrow_max rows, which the
-    // narrow kernel takes (their count goes to narrow_info[0]).
-    // Tiles of nearly equal cost sit together in the grouped GEMMs' schedule,
-    // so the workgroups that share a tile block stay in step and reuse its
-    // operands in L2, and a large expert's partial tile runs while its
-    // weights are still in L2 / MALL instead of streaming them once more.
-    const int q_full = cnt / tile_m;
-    const int q_part = (cnt % tile_m) ? 1 : 0;
-    const int q_head = q_full > 0 ? q_full + q_part : 0;
-    const int q_narrow = (q_full == 0 && cnt > 0 && cnt <= narrow_max) ? 1 : 0;
-    const int q_tail = (q_full > 0 || q_narrow) ? 0 : q_part;
-    const int head_base = block_exclusive_scan(q_head, wave_tot);
-    const int tail_base = block_exclusive_scan(q_tail, wave_tot);
-    const int narrow_base = block_exclusive_scan(q_narrow, wave_tot);
-    __shared__ int n_head, n_tail;
-    if (part == 0 && e == num_experts - 1) {
-      n_head = head_base + q_head;
-      n_tail = tail_base + q_tail;
-      if (narrow_info != nullptr) narrow_info[0] = narrow_base + q_narrow;
+  if (lane == 63) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) wave_tot[wave][i] = incl[i];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int nw = blockDim.x >> 6;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int wv = lane < nw ? wave_tot[lane][i] : 0;
+      int wi = wv;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int n = __shfl_up(wi, o, 64);
+        if (lane >= o) wi += n;
+      }
+      if (lane < nw) wave_tot[lane][i] = wi - wv;
     }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = wave_tot[wave][i] + incl[i] - v[i];
+}
+
+__global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
+    int num_experts, const int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ mtile_offsets, int32_t* __restrict__ mtile_list, int tile_m,
+    float* amax_reset, int32_t* tile_counters, int narrow_max, int32_t* narrow_info) {
+  __shared__ int wave_tot[kScanThreads / 64][5];
+  __shared__ int n_head, n_tail;
+  const int e = threadIdx.x;  // E <= kScanThreads
+  const int cnt = (e < num_experts) ? counts[e] : 0;
+  const int mt = (cnt + tile_m - 1) / tile_m;
+  // M-tile list [(expert, first row)]: first the experts with at least one
+  // full tile, each with all its tiles (full ones, then its partial one), in
+  // expert order; then the single partial tiles of the smaller experts; last,
+  // with narrow_max > 0, the experts of 1..narrow_max rows, which the narrow
+  // kernel takes (their count goes to narrow_info[0]).  Tiles of nearly equal
+  // cost sit together in the grouped GEMMs' schedule, so the workgroups that
+  // share a tile block stay in step and reuse its operands in L2, and a large
+  // expert's partial tile runs while its weights are still in L2 / MALL
+  // instead of streaming them once more.
+  const int q_full = cnt / tile_m;
+  const int q_part = (cnt % tile_m) ? 1 : 0;
+  const int q_head = q_full > 0 ? q_full + q_part : 0;
+  const int q_narrow = (q_full == 0 && cnt > 0 && cnt <= narrow_max) ? 1 : 0;
+  const int q_tail = (q_full > 0 || q_narrow) ? 0 : q_part;
+  // one pass of exclusive scans over the experts: row offsets, M-tile
+  // offsets, and the list positions of the three kinds of tiles
+  int sc[5] = {cnt, mt, q_head, q_tail, q_narrow};
+  block_exclusive_scan_n<5>(sc, wave_tot);
+  const int off = sc[0], moff = sc[1], head_base = sc[2], tail_base = sc[3], narrow_base = sc[4];
+  if (e < num_experts) {
+    offsets[e] = off;
+    mtile_offsets[e] = moff;
+  }
+  if (e == num_experts - 1) {
+    offsets[num_experts] = off + cnt;
+    mtile_offsets[num_experts] = moff + mt;
+    n_head = head_base + q_head;
+    n_tail = tail_base + q_tail;
+    if (mtile_list != nullptr && narrow_info != nullptr) narrow_info[0] = narrow_base + q_narrow;
+  }
+  if (mtile_list != nullptr) {
     __syncthreads();
-    if (part == 0 && e < num_experts) {
+    if (e < num_experts) {
       for (int s = 0; s < q_head; ++s) {
         mtile_list[2 * (head_base + s)] = e;
         mtile_list[2 * (head_base + s) + 1] = off + s * tile_m;
@@ -227,6 +289,7 @@ __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
       }
     }
   }
+  const int tid = threadIdx.x;
   if (narrow_info != nullptr && tid >= 1 && tid < 1 + kNarrowCounters) narrow_info[tid] = 0;
   if (tid == 0 && amax_reset != nullptr) *amax_reset = 0.0f;
   if (tile_counters != nullptr && tid < kTileCounters) tile_counters[tid] = 0;
