@@ -563,8 +563,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 
   // The next tile is found during a tile's K loop by thread 0, one memory
   // round trip per K step, each looked at only after the step's own DMA wait
-  // (which covers it): step 1 claims a slot, its end turns the slot into
-  // (m, n) and loads the M tile's (expert, first row); step 2's end loads the
+  // (which covers it): the slot's atomic was issued before the tile began;
+  // step 1's end turns the slot into (m, n) and loads the M tile's (expert,
+  // first row); step 2's end loads the
   // expert's row offsets; step 3's end publishes the tile in LDS.  Step
   // k_steps - 3 reads it and DMAs its gathered rows and weight scales into
   // LDS; its first stages are loaded by the last K steps like any other step:
@@ -582,6 +583,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   if (cur.t < 0) return;
   int buf = 0, gstep = 0;
   start_tile(cur, buf, gstep);
+  // thread 0: the claim slot that step 1 of the current tile turns into the
+  // next tile.  With kEarlyClaim its atomic is issued before the tile starts
+  // (here, then at the end of each epilogue), so it has two K steps to return
+  // instead of one; it pays where tiles are short (GEMM 2: 16 K steps, 2.7%),
+  // while in GEMM 1 the register it keeps across the tile loop cost more
+  // (+1.8%: scalar spills reached the loop of plain steps), so there step 1
+  // issues it.
+  constexpr bool kEarlyClaim = (EPI == Epi::kStoreBf16);
+  int q_j_next = 0;
+  if (kEarlyClaim && pipe && tid == 0) q_j_next = claim_start();
 
   while (true) {
     if (grp == 1) sync_lds();  // group 1 runs one phase behind group 0
@@ -589,7 +600,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     const int live_sub = max(0, min(8, (cur.valid - wave_row0 + 15) >> 4));
     Tile nxt{-1, 0, 0, 0, 0, 0};
     // thread 0's lookups of the next tile (meaningful in lane 0 only)
-    int q_j = 0, q_m = -1, q_n = 0, q_e = 0, q_row0 = 0, q_end = 0, q_beg = 0, q_mt = 0;
+    int q_j = q_j_next, q_m = -1, q_n = 0, q_e = 0, q_row0 = 0, q_end = 0, q_beg = 0, q_mt = 0;
 
     f32x4 acc[8][4];
 #pragma unroll
@@ -632,10 +643,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         // into the previous step's stage, whose reads all ended with that step
         if (nxt.t >= 0) issue_a(0, stg ^ 1, nxt.valid);
       }
-      if constexpr (MODE == kClaim) {
+      if constexpr (MODE == kClaim && !kEarlyClaim) {
         if (tid == 0) q_j = claim_start();
       }
-
       // ---- memory phase 1: B fragments, A sub-tiles 0-3, scales, DMA kt+1
       i32x8 bf[4], af[4];
       int mx_sb = 0, mx_sa0 = 0, mx_sa1 = 0;
@@ -1030,6 +1040,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     }
 
     if (nxt.t < 0) break;
+    // the claim for the tile after nxt, behind this epilogue's stores (a claim
+    // issued before them would make the epilogue's first LDS store, which the
+    // compiler orders after all outstanding vector memory, wait for it)
+    if (kEarlyClaim && pipe && tid == 0) q_j_next = claim_start();
     if (!pipe) start_tile(nxt, buf ^ 1, gstep + k_steps);
     cur = nxt;
     buf ^= 1;
