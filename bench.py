@@ -77,6 +77,10 @@ def parse():
                          "so that no launch finds its operands in L2/MALL (0: one copy)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (counter calibration)")
+    ap.add_argument("--other-configs", default="mixtral,decode,dense2048,tp_local",
+                    help="default dsv3 run only: also measure these workloads (each in a child process, "
+                         "10 steps, no CPU baseline) and attach their results as `other_configs`; "
+                         "'' to skip")
     ap.add_argument("--summarize-counters", metavar="DIR", default=None,
                     help="no GPU work: turn the rocprofv3 --pmc output under DIR (mfma/, lds/) of this config "
                          "into profiles/*_counters.md")
@@ -983,7 +987,37 @@ def main():
         res.pop("gemm_only_tflops")
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(inp, cfg, args.cpu_seconds)
+    if args.config == "dsv3" and args.other_configs:
+        res["other_configs"] = other_configs(args)
     print(json.dumps(res), flush=True)
+
+
+def other_configs(args):
+    """Configs 1, 2, 4 and 5 (parity-test cases, not the headline): each runs as
+    `bench.py --config <w>` in a child process (its own GPU memory, 10 timed
+    steps after 3 warm-up steps, no CPU baseline); the fields that describe
+    the result are kept."""
+    import subprocess
+    out = {}
+    for name in [c for c in args.other_configs.split(",") if c]:
+        cmd = [sys.executable, os.path.abspath(__file__), "--config", name, "--steps", "10", "--warmup", "3",
+               "--no-cpu", "--other-configs", ""]
+        try:
+            p = subprocess.run(cmd, capture_output=True, text=True, timeout=240)
+            line = [ln for ln in p.stdout.splitlines() if ln.startswith("{")]
+            if p.returncode != 0 or not line:
+                out[name] = {"error": f"exit {p.returncode}: {p.stderr.strip()[-300:]}"}
+                continue
+            d = json.loads(line[-1])
+        except subprocess.TimeoutExpired:
+            out[name] = {"error": "timed out"}
+            continue
+        keep = {k: d[k] for k in ("value", "unit", "ms_per_step", "pct_fp8_peak", "eager_ms_per_step") if k in d}
+        keep["workload"] = d["config"]["workload"]
+        rf = d.get("roofline", {})
+        keep["roofline"] = {k: rf[k] for k in ("kernel", "bound", "achieved", "unit", "frac", "avg_ms") if k in rf}
+        out[name] = keep
+    return out
 
 
 if __name__ == "__main__":
