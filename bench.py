@@ -484,11 +484,11 @@ def cpu_baseline(inp, cfg, budget_s):
 # rocprofv3 summaries (host only)
 # ----------------------------------------------------------------------------
 PROF_TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d {d}/trace -o run -- "
-                  "python3 bench.py --config {c} --steps 5 --warmup 2 --no-cpu > {d}/bench.json")
+                  "python3 bench.py --config {c} --steps 5 --warmup 2 --no-cpu --other-configs '' > {d}/bench.json")
 PROF_TRACE_CMD_DENSE = ("rocprofv3 --kernel-trace --stats --output-format csv -d {d}/trace -o run -- "
                         "python3 bench.py --config {c} --steps 40 --warmup 5 --no-cpu > {d}/bench.json")
 PROF_PMC_CMD = ("rocprofv3 --pmc {ctr} --output-format csv -d {d}/{ctr} -o run -- "
-                "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu --calibrate-copy")
+                "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu --other-configs '' --calibrate-copy")
 CALIB_BYTES = 1 << 30
 
 
@@ -544,6 +544,33 @@ def _algorithmic_bytes(cfg, active, narrow=None):
     return {"grouped_gemm1": g1, "grouped_gemm2": g2, "combine": comb}
 
 
+def _write_timeline(f, path, n_calls):
+    """The last timed one-call layer of a kernel trace (the n_calls-th routing
+    launch opens it, the next one closes it): each kernel's start and end
+    relative to the layer's first launch, and the CUs' idle windows it shows."""
+    import csv
+    if not os.path.exists(path):
+        return
+    with open(path) as tf:
+        ks = sorted(csv.DictReader(tf), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(ks) if "route_topk" in r["Kernel_Name"]]
+    if len(starts) < n_calls:
+        return
+    i0 = starts[n_calls - 1]
+    i1 = starts[n_calls] if len(starts) > n_calls else len(ks)
+    t0 = int(ks[i0]["Start_Timestamp"])
+    f.write("\nTimeline of the last timed layer call (one `MoELayer` call: the narrow kernels run on the "
+            "library's auxiliary stream beside the 256x256 GEMMs):\n\n")
+    f.write("| kernel | start us | end us | duration us |\n|---|---|---|---|\n")
+    for r in ks[i0:i1]:
+        lab = _kernel_label(r["Kernel_Name"], False)
+        if lab is None:  # torch's own kernels between calls
+            continue
+        s0 = (int(r["Start_Timestamp"]) - t0) / 1e3
+        s1 = (int(r["End_Timestamp"]) - t0) / 1e3
+        f.write(f"| {lab} | {s0:.1f} | {s1:.1f} | {s1 - s0:.1f} |\n")
+
+
 def summarize_profile(args):
     import csv
     import collections
@@ -588,6 +615,8 @@ def summarize_profile(args):
         f.write("| kernel | calls | avg us | min us | max us | share of library time |\n|---|---|---|---|---|---|\n")
         for lab, n, avg, mn, mx, t in sorted(rows, key=lambda r: -r[5]):
             f.write(f"| {lab} | {n} | {avg:.1f} | {mn:.1f} | {mx:.1f} | {100 * t / tot:.1f}% |\n")
+        if not dense:
+            _write_timeline(f, os.path.join(d, "trace", "run_kernel_trace.csv"), b["warmup"] + b["steps"])
     # traffic passes
     per = {}
     calib = {}
@@ -668,7 +697,7 @@ PMC_PASSES = {
     "lds": "LDSBankConflict LdsBankConflict SQ_INSTS_LDS SQ_WAIT_INST_LDS SQ_LDS_IDX_ACTIVE",
 }
 PROF_PMC_PASS_CMD = ("rocprofv3 --pmc {ctrs} --output-format csv -d {d}/{p} -o run -- "
-                     "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu")
+                     "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu --other-configs ''")
 
 
 def summarize_counters(args):
