@@ -684,7 +684,17 @@ int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, i
   HK_REQUIRE(hidden > 0 && hidden % 8 == 0, "combine: hidden=%d must be a multiple of 8", hidden);
   HK_REQUIRE(num_tokens >= 0 && num_tokens < (1ll << 31), "combine: bad T");
   if (num_tokens == 0) return HKMOE_OK;
-  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(num_tokens)), dim3(256), 0,
+  // the largest multiple of 64 threads (<= 512) that divides the row's 16-byte
+  // chunks, so no workgroup ends on a partly idle pass (H = 7168: 448 threads
+  // and two passes instead of 256 and a half-empty fourth); 256 otherwise
+  const int chunks = hidden / 8;
+  int threads = 256;
+  for (int t = 512; t >= 64; t -= 64)
+    if (chunks % t == 0) {
+      threads = t;
+      break;
+    }
+  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(num_tokens)), dim3(threads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(y), topk_w,
                      inv_perm, top_k, hidden, static_cast<uint16_t*>(out));
   return check_launch("combine_kernel");

@@ -418,11 +418,12 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
 
 // ---------------------------------------------------------------------------
 // 5. combine: out[t] = bf16(sum_j w[t,j] * y[inv_perm[t*k+j]]), one
-//    workgroup per token, 8 columns (16 bytes) per thread and step.  The
+//    workgroup per token, 8 columns (16 bytes) per thread and step (the
+//    host sizes the workgroup so the row's 16-byte chunks divide evenly).  The
 //    token's weights and y rows are staged in LDS once; the y loads of up to
 //    8 slots are issued together, then summed in slot order j = 0 .. k-1.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
+__global__ __launch_bounds__(512) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const float* __restrict__ topk_w,
                                                       const int32_t* __restrict__ inv_perm,
                                                       int top_k, int hidden,
@@ -436,7 +437,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   }
   __syncthreads();
   const int cols8 = hidden / 8;
-  for (int c = threadIdx.x; c < cols8; c += 256) {
+  for (int c = threadIdx.x; c < cols8; c += blockDim.x) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j0 = 0; j0 < top_k; j0 += 8) {
       uint4 v[8];
