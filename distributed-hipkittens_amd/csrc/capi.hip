@@ -677,6 +677,13 @@ int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k,
   return check_launch("pack_weights_kernel");
 }
 
+int hkmoe_requant_quotient_check(int32_t* counts, hkmoe_stream_t stream) {
+  HK_REQUIRE(counts, "requant_quotient_check: null pointer");
+  hipLaunchKernelGGL(requant_quotient_check_kernel, dim3(128, 37 + 27), dim3(128), 0,
+                     static_cast<hipStream_t>(stream), counts);
+  return check_launch("requant_quotient_check_kernel");
+}
+
 int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, int64_t num_tokens,
                   int32_t top_k, int32_t hidden, void* out, hkmoe_stream_t stream) {
   HK_REQUIRE(y && topk_w && inv_perm && out, "combine: null pointer");

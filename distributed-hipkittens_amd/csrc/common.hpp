@@ -124,6 +124,41 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
 // gate/up GEMM's epilogue of a 256x256 tile.
 __device__ __forceinline__ float quot_e4m3(float x, float s) { return x / s; }
 
+// The e4m3 byte of fl(x / s) computed without a division per value.  Per
+// scale (QuotScale): s is brought into [1, 2) by an exact power of two 2^sh,
+// and y = fl(1 / s') is its correctly rounded reciprocal.  Per value: x' = x
+// 2^sh (exact: |x| <= 448 s, so x' <= 2^10), q0 = fl(x' y) is within one ulp
+// of x'/s', the remainder x' - q0 s' is exact in one FMA, and fl(q0 + r y) is
+// then the correctly rounded x'/s' = x/s (Markstein's theorem: P. Markstein,
+// "Computation of elementary functions on the IBM RISC System/6000 processor",
+// IBM J. Res. Dev. 34(1), 1990; restated in J.-M. Muller et al., Handbook of
+// Floating-Point Arithmetic, 2nd ed., section 4.7).  The scaling keeps the
+// remainder clear of underflow for every quotient of at least 2^-10, the
+// smallest that rounds to a nonzero e4m3 value; unscaled, tiny x and s gave
+// wrong corrections.  One ldexp, a product and two FMAs per value instead of
+// the division's eleven dependent operations; hkmoe_requant_quotient_check
+// compares the e4m3 bytes with those of x / s over every bf16 x and bf16 row
+// maximum the GEMM epilogues can see.
+struct QuotScale {
+  float s1;  // s 2^sh, in [1, 2)
+  float y;   // fl(1 / s1)
+  int sh;
+};
+__device__ __forceinline__ QuotScale quot_scale(float s) {
+  const int sh = 1 - __builtin_amdgcn_frexp_expf(s);  // s = m 2^e, m in [0.5, 1)
+  const float s1 = __builtin_amdgcn_ldexpf(s, sh);
+  return QuotScale{s1, 1.0f / s1, sh};
+}
+__device__ __forceinline__ float quot_e4m3(float x, const QuotScale& q) {
+#pragma clang fp contract(off)
+  const float x1 = __builtin_amdgcn_ldexpf(x, q.sh);
+  const float q0 = x1 * q.y;
+  const float r = __builtin_fmaf(-q0, q.s1, x1);
+  // s > 0, so the quotient has x's sign; this also keeps -0 / s = -0, which
+  // q0 + r*y = -0 + +0 would turn into +0
+  return __builtin_copysignf(__builtin_fmaf(r, q.y, q0), x);
+}
+
 // Four finite fp32 -> four e4m3fn bytes (a in bits 0-7), round to nearest
 // even, saturating at +-448: a clamp to [-448, 448] and two hardware packed
 // conversions.  (The conversion alone rounds exactly like f32_to_e4m3 for

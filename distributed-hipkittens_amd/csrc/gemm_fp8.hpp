@@ -1015,12 +1015,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
           if (i < live_sub) {
             const f32x4 mm = *reinterpret_cast<const f32x4*>(rmax + r * 4);
             const float s = scale_from_amax(fmaxf(fmaxf(mm.x, mm.y), fmaxf(mm.z, mm.w)));
+            const QuotScale qs = quot_scale(s);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
               const int c = wg * 2 + j;
               *reinterpret_cast<uint32_t*>(ct + r * 128 + ((c ^ (r & 7)) << 4) + elg * 4) =
-                  pack_e4m3x4(quot_e4m3(acc[i][j][0], s), quot_e4m3(acc[i][j][1], s),
-                              quot_e4m3(acc[i][j][2], s), quot_e4m3(acc[i][j][3], s));
+                  pack_e4m3x4(quot_e4m3(acc[i][j][0], qs), quot_e4m3(acc[i][j][1], qs),
+                              quot_e4m3(acc[i][j][2], qs), quot_e4m3(acc[i][j][3], qs));
             }
             if (wg == 0 && elg == 0 && r < valid) p.c_scale[static_cast<int64_t>(nt) * p.rows + row0 + r] = s;
           }

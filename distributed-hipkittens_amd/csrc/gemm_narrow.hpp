@@ -497,14 +497,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
         for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         if (live) {
           const float sc = scale_from_amax(m);
+          const QuotScale qs = quot_scale(sc);
           uint32_t qw[2];
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2) {
             const uint32_t lo = w[2 * h2], hi = w[2 * h2 + 1];
-            qw[h2] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(lo & 0xffffu), sc),
-                                 quot_e4m3(bf16_bits_to_f32(lo >> 16), sc),
-                                 quot_e4m3(bf16_bits_to_f32(hi & 0xffffu), sc),
-                                 quot_e4m3(bf16_bits_to_f32(hi >> 16), sc));
+            qw[h2] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(lo & 0xffffu), qs),
+                                 quot_e4m3(bf16_bits_to_f32(lo >> 16), qs),
+                                 quot_e4m3(bf16_bits_to_f32(hi & 0xffffu), qs),
+                                 quot_e4m3(bf16_bits_to_f32(hi >> 16), qs));
           }
           uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(C.row0 + r) * p.n_out + C.nt * 128 + q * 8;
           *reinterpret_cast<uint2*>(dst) = uint2{qw[0], qw[1]};

@@ -468,6 +468,52 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// Self-check of the epilogues' requantisation quotient: quot_e4m3(x, qs)
+// against the correctly rounded x / s for every input the GEMM epilogues can
+// produce: x a bf16 value, s = scale_from_amax(amax) with amax a bf16 value
+// >= |x|.  Both quotients scale exactly with powers of two, so the check
+// enumerates mantissas and sampled exponents: blocks (ma, ea) with amax =
+// (1 + ma/128) 2^ea, ea = -126, -119, ..., 126; threads mx; each thread tries
+// x = +-(1 + mx/128) 2^(ea - g), g = 0 .. 40 (x <= amax, x normal), and, in
+// blocks with y >= 37, bf16 subnormals and zeros x = +-mx 2^-133 against amax
+// with ea in [-126, -100].  counts[0] += cases, counts[1] += mismatches: e4m3
+// bytes that differ, or fp32 quotients that differ where |x / s| >= 2^-10
+// (signed zeros included).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(128) void requant_quotient_check_kernel(int* __restrict__ counts) {
+  const int ma = blockIdx.x, mx = threadIdx.x;
+  const bool sub = blockIdx.y >= 37;
+  const int ea = sub ? -126 + static_cast<int>(blockIdx.y - 37) : -126 + 7 * static_cast<int>(blockIdx.y);
+  const float amax = __builtin_amdgcn_ldexpf(1.0f + ma / 128.0f, ea);
+  const float s = scale_from_amax(amax);
+  const QuotScale qs = quot_scale(s);
+  int cases = 0, bad = 0;
+  for (int g = 0; g <= (sub ? 0 : 40); ++g) {
+    float x;
+    if (sub) {
+      x = __builtin_amdgcn_ldexpf(static_cast<float>(mx), -133);  // mx = 0: +-0
+    } else {
+      if (ea - g < -126) break;
+      if (g == 0 && mx > ma) continue;  // x <= amax
+      x = __builtin_amdgcn_ldexpf(1.0f + mx / 128.0f, ea - g);
+    }
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg) {
+      const float xv = sg ? -x : x;
+      const float qd = quot_e4m3(xv, s), qm = quot_e4m3(xv, qs);
+      // the stored e4m3 bytes must agree, and the fp32 quotients too wherever
+      // they can round to a nonzero e4m3 value
+      const bool same_byte = (pack_e4m3x4(qd, 0.0f, 0.0f, 0.0f) & 0xffu) == (pack_e4m3x4(qm, 0.0f, 0.0f, 0.0f) & 0xffu);
+      const bool same_bits = __float_as_uint(qd) == __float_as_uint(qm) || fabsf(qd) < 0.0009765625f;
+      bad += !(same_byte && same_bits);
+      ++cases;
+    }
+  }
+  atomicAdd(&counts[0], cases);
+  atomicAdd(&counts[1], bad);
+}
+
+// ---------------------------------------------------------------------------
 // 6. quantisers (fp32 input) used to build e4m3 operands on the device
 // ---------------------------------------------------------------------------
 // 1x128 groups, row-major scales [R, C/128]; one wave per group.

@@ -281,6 +281,15 @@ void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gathe
                             static_cast<float*>(aux.ptr), static_cast<int32_t*>(tc.ptr), current_stream()));
 }
 
+// counts [2] int32 (zeroed by the caller) += (cases, mismatches) of the
+// requantisation-quotient self-check (hkmoe_requant_quotient_check)
+void dispatch_requant_quotient_check(py::object counts) {
+  auto c = as_tensor(counts, "counts");
+  want_dtype(c, "counts", kI32);
+  if (c.numel() != 2) throw std::runtime_error("counts must hold two int32");
+  check(hkmoe_requant_quotient_check(static_cast<int32_t*>(c.ptr), current_stream()));
+}
+
 void dispatch_requant(py::object h, py::object amax, py::object hq, py::object hs) {
   auto hh = as_tensor(h, "h"), am = as_tensor_opt(amax, "amax"), q = as_tensor(hq, "hq"),
        s = as_tensor(hs, "hs");
@@ -666,6 +675,7 @@ PYBIND11_MODULE(tk_kernel, m) {
         py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none(),
         py::arg("narrow_info") = py::none(), py::arg("part") = 0, py::arg("grid") = 0);
   m.def("dispatch_requant", &dispatch_requant);
+  m.def("dispatch_requant_quotient_check", &dispatch_requant_quotient_check);
   m.def("dispatch_grouped_gemm2", &dispatch_grouped_gemm2, py::arg("hq"), py::arg("hs"), py::arg("w2"),
         py::arg("w2_scale"), py::arg("offsets"), py::arg("mtile_offsets"), py::arg("y"),
         py::arg("tile_counters") = py::none(), py::arg("packed") = false, py::arg("mtile_list") = py::none(),

@@ -227,6 +227,22 @@ int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k,
                        void* packed, hkmoe_stream_t stream);
 
 /*
+ * Self-check of the requantisation quotient used by the GEMM 1 epilogues
+ * (256x256 and narrow kernels): each value x of a 1x128 group is divided by its
+ * scale s without a division per value (x and s scaled by one power of two so
+ * that s is in [1, 2), fl(x*y) with y = fl(1/s), one exact-remainder FMA
+ * correction).  This launches one kernel that compares the result with the
+ * IEEE quotient x / s over every input those epilogues can produce (x a bf16
+ * value, s = max(amax/448, 2^-126) with amax a bf16 value >= |x|; mantissas
+ * exhaustive, exponents sampled, both signs, bf16 subnormals and signed zeros):
+ * the e4m3 bytes must agree, and the fp32 quotients wherever |x/s| >= 2^-10.
+ * counts [2] int32 on the device, zeroed by the caller: counts[0] += cases,
+ * counts[1] += mismatches.
+ * No reference counterpart (the reference has no requantisation step).
+ */
+int hkmoe_requant_quotient_check(int32_t* counts, hkmoe_stream_t stream);
+
+/*
  * Top-k weighted unpermute/combine:
  *   out[t] = bf16( sum_{j<k} topk_w[t,j] * y[inv_perm[t*k+j]] ), fp32 accumulate.
  *   y [T*k, H] bf16, out [T, H] bf16, H % 8 == 0.

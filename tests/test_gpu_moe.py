@@ -187,12 +187,40 @@ def test_mtile_list_order_and_results(hk, name):
     del e
 
 
+def _quotient_check_cases():
+    """The number of (x, s) pairs hkmoe_requant_quotient_check enumerates."""
+    n = 0
+    for y in range(37):  # normal x: ea = -126 + 7y, g = 0 .. 40 with x >= 2^-126, x <= amax
+        ea = -126 + 7 * y
+        for ma in range(128):
+            for g in range(41):
+                if ea - g < -126:
+                    break
+                n += 2 * (ma + 1 if g == 0 else 128)
+    n += 27 * 128 * 128 * 2  # bf16 subnormals and zeros x = +-mx 2^-133, amax exponents -126 .. -100
+    return n
+
+
+def test_requant_quotient_matches_division(hk):
+    """The GEMM 1 epilogues divide each value by its group scale as a product
+    with the correctly rounded reciprocal plus one exact-remainder FMA step.
+    That must give the IEEE quotient bit for bit (the requantisation is
+    bit-exact against the oracle): checked on the device over every bf16 value
+    against every bf16 row maximum, exponents sampled across the range."""
+    counts = torch.zeros(2, dtype=torch.int32, device="cuda")
+    hk.tk_kernel.dispatch_requant_quotient_check(counts)
+    torch.cuda.synchronize()
+    cases, bad = (int(v) for v in counts.cpu())
+    assert cases == _quotient_check_cases()
+    assert bad == 0, f"{bad} of {cases} quotients differ from x / s"
+
+
 @pytest.mark.parametrize("block", [True, False])
 def test_requant_large_bit_exact(hk, block):
     """Requantisation of 8M bf16 values (log-normal row magnitudes, plus rows
     whose values sit on and next to e4m3 rounding midpoints) is bit-exact
-    against the oracle: the quotient x / s is taken as a product with 1 / s
-    except near midpoints, and this exercises both paths."""
+    against the oracle (the quotient x / s correctly rounded, then RNE to
+    e4m3, including the ties at midpoints)."""
     rng = np.random.default_rng(31)
     rows, inter = 4096, 2048
     h = rng.standard_normal((rows, inter)).astype(np.float32)
