@@ -695,6 +695,7 @@ PMC_PASSES = {
     "mfma": "MfmaUtil VALUBusy SQ_VALU_MFMA_COEXEC_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F8 "
             "SQ_BUSY_CYCLES",
     "lds": "LDSBankConflict LdsBankConflict SQ_INSTS_LDS SQ_WAIT_INST_LDS SQ_LDS_IDX_ACTIVE",
+    "mem": "TCP_TCC_READ_REQ_LATENCY_sum TCP_TCC_READ_REQ_sum TCP_PENDING_STALL_CYCLES_sum GRBM_GUI_ACTIVE",
 }
 PROF_PMC_PASS_CMD = ("rocprofv3 --pmc {ctrs} --output-format csv -d {d}/{p} -o run -- "
                      "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu --other-configs ''")
@@ -730,7 +731,7 @@ def summarize_counters(args):
     with open(out, "w") as f:
         f.write(f"# rocprofv3 counters: {'dense GEMM' if dense else 'MoE layer'}, workload `{args.config}`\n\n")
         f.write(f"Config: {json.dumps(cfg)}\n\n")
-        f.write("Two counter passes, one rocprofv3 run each (repo root):\n\n")
+        f.write(f"{len(PMC_PASSES)} counter passes, one rocprofv3 run each (repo root):\n\n")
         for p, ctrs in PMC_PASSES.items():
             f.write("    " + PROF_PMC_PASS_CMD.format(ctrs=ctrs, d="<out>", p=p, c=args.config) + "\n")
         f.write("\nCounter collection serialises the dispatches, so every kernel runs alone on the GPU "
@@ -757,6 +758,26 @@ def summarize_counters(args):
                        else "-")
                     + f" | {g('LDSBankConflict', '{:.2f}')} | {g('LdsBankConflict', '{:.4f}')} | "
                     + f"{g('SQ_INSTS_LDS', '{:,.0f}')} |\n")
+        if any("TCP_TCC_READ_REQ_sum" in a for a in avg.values()):
+            f.write("\nMemory side (pass `mem`): L2 read latency = TCP_TCC_READ_REQ_LATENCY_sum / "
+                    "TCP_TCC_READ_REQ_sum, in cycles as the CU's L1 (TCP) sees them; requests are 128 B. GPU "
+                    "cycles = GRBM_GUI_ACTIVE / 8 (one count per XCD). In flight = requests per GPU cycle x "
+                    "latency (Little's law), per CU of the kernel. TCP pending stall = "
+                    "TCP_PENDING_STALL_CYCLES_sum / (GPU cycles x CUs of the kernel): the share of cycles an "
+                    "L1 waits on data from L2.\n\n")
+            f.write("| kernel | CUs | L2 read requests | L2 read latency (cycles) | GPU cycles | requests in flight "
+                    "per CU | TCP pending stall % |\n|---|---|---|---|---|---|---|\n")
+            ncu = {"grouped_gemm1": 192, "narrow_gemm1": 64, "narrow_gemm2": 64}
+            for lab in sorted(avg, key=lambda x: -avg[x].get("TCP_TCC_READ_REQ_sum", 0)):
+                a = avg[lab]
+                req, lat = a.get("TCP_TCC_READ_REQ_sum", 0.0), a.get("TCP_TCC_READ_REQ_LATENCY_sum", 0.0)
+                cyc = a.get("GRBM_GUI_ACTIVE", 0.0) / 8
+                if req < 1e5 or cyc <= 0:
+                    continue
+                cus = ncu.get(lab, 256) if not dense else 256
+                f.write(f"| {lab} | {cus} | {req:,.0f} | {lat / req:.0f} | {cyc:,.0f} | "
+                        f"{req / cyc / cus * lat / req:.0f} | "
+                        f"{100 * a.get('TCP_PENDING_STALL_CYCLES_sum', 0.0) / (cyc * cus):.0f} |\n")
     print(json.dumps({"written": [os.path.relpath(out, ROOT)]}))
 
 
