@@ -679,7 +679,7 @@ int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k,
 
 int hkmoe_requant_quotient_check(int32_t* counts, hkmoe_stream_t stream) {
   HK_REQUIRE(counts, "requant_quotient_check: null pointer");
-  hipLaunchKernelGGL(requant_quotient_check_kernel, dim3(128, 37 + 27), dim3(128), 0,
+  hipLaunchKernelGGL(requant_quotient_check_kernel, dim3(128, 37 + 27 + 1), dim3(128), 0,
                      static_cast<hipStream_t>(stream), counts);
   return check_launch("requant_quotient_check_kernel");
 }

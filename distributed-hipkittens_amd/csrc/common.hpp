@@ -145,9 +145,12 @@ struct QuotScale {
   int sh;
 };
 __device__ __forceinline__ QuotScale quot_scale(float s) {
-  const int sh = 1 - __builtin_amdgcn_frexp_expf(s);  // s = m 2^e, m in [0.5, 1)
-  const float s1 = __builtin_amdgcn_ldexpf(s, sh);
-  return QuotScale{s1, 1.0f / s1, sh};
+  // s = +inf (a row whose h overflowed): s' = 1, y = 0, no shift give x / inf
+  // exactly (q0 = 0, r = x, q = +-0; an infinite x gives NaN)
+  const bool inf = __builtin_isinf(s);
+  const int sh = inf ? 0 : 1 - __builtin_amdgcn_frexp_expf(s);  // s = m 2^e, m in [0.5, 1)
+  const float s1 = inf ? 1.0f : __builtin_amdgcn_ldexpf(s, sh);
+  return QuotScale{s1, inf ? 0.0f : 1.0f / s1, sh};
 }
 __device__ __forceinline__ float quot_e4m3(float x, const QuotScale& q) {
 #pragma clang fp contract(off)

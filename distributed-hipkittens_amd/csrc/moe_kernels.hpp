@@ -475,13 +475,35 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t* __restrict
 // enumerates mantissas and sampled exponents: blocks (ma, ea) with amax =
 // (1 + ma/128) 2^ea, ea = -126, -119, ..., 126; threads mx; each thread tries
 // x = +-(1 + mx/128) 2^(ea - g), g = 0 .. 40 (x <= amax, x normal), and, in
-// blocks with y >= 37, bf16 subnormals and zeros x = +-mx 2^-133 against amax
-// with ea in [-126, -100].  counts[0] += cases, counts[1] += mismatches: e4m3
-// bytes that differ, or fp32 quotients that differ where |x / s| >= 2^-10
-// (signed zeros included).
+// blocks with y in 37 .. 63, bf16 subnormals and zeros x = +-mx 2^-133
+// against amax with ea in [-126, -100]; blocks with y = 64, amax = +inf (a row
+// whose h overflowed) against finite and infinite x.  counts[0] += cases,
+// counts[1] += mismatches: e4m3 bytes that differ, or fp32 quotients that
+// differ where |x / s| >= 2^-10 (signed zeros included; two NaNs agree).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(128) void requant_quotient_check_kernel(int* __restrict__ counts) {
   const int ma = blockIdx.x, mx = threadIdx.x;
+  if (blockIdx.y == 64) {
+    // a row whose h overflowed: amax = +inf, s = +inf; x = +-(1 + mx/128) 2^e for
+    // e = -126 + ma*2 (block ma < 127), or x = +-inf (block 127, thread 0)
+    const QuotScale qs = quot_scale(scale_from_amax(__builtin_inff()));
+    const float s = scale_from_amax(__builtin_inff());
+    int cases = 0, bad = 0;
+    if (ma < 127 || mx == 0) {
+      const float x = ma < 127 ? __builtin_amdgcn_ldexpf(1.0f + mx / 128.0f, -126 + 2 * ma) : __builtin_inff();
+#pragma unroll
+      for (int sg = 0; sg < 2; ++sg) {
+        const float xv = sg ? -x : x;
+        const float qd = quot_e4m3(xv, s), qm = quot_e4m3(xv, qs);
+        // both NaN (inf / inf; its sign is not specified), or the same bits
+        bad += !((__builtin_isnan(qd) && __builtin_isnan(qm)) || __float_as_uint(qd) == __float_as_uint(qm));
+        ++cases;
+      }
+    }
+    atomicAdd(&counts[0], cases);
+    atomicAdd(&counts[1], bad);
+    return;
+  }
   const bool sub = blockIdx.y >= 37;
   const int ea = sub ? -126 + static_cast<int>(blockIdx.y - 37) : -126 + 7 * static_cast<int>(blockIdx.y);
   const float amax = __builtin_amdgcn_ldexpf(1.0f + ma / 128.0f, ea);

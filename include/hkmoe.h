@@ -234,7 +234,8 @@ int hkmoe_pack_weights(const void* w, int64_t num_experts, int64_t n, int64_t k,
  * correction).  This launches one kernel that compares the result with the
  * IEEE quotient x / s over every input those epilogues can produce (x a bf16
  * value, s = max(amax/448, 2^-126) with amax a bf16 value >= |x|; mantissas
- * exhaustive, exponents sampled, both signs, bf16 subnormals and signed zeros):
+ * exhaustive, exponents sampled, both signs, bf16 subnormals and signed zeros,
+ * amax = inf):
  * the e4m3 bytes must agree, and the fp32 quotients wherever |x/s| >= 2^-10.
  * counts [2] int32 on the device, zeroed by the caller: counts[0] += cases,
  * counts[1] += mismatches.

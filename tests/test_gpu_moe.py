@@ -198,6 +198,7 @@ def _quotient_check_cases():
                     break
                 n += 2 * (ma + 1 if g == 0 else 128)
     n += 27 * 128 * 128 * 2  # bf16 subnormals and zeros x = +-mx 2^-133, amax exponents -126 .. -100
+    n += 127 * 128 * 2 + 2  # amax = inf: finite x, and x = +-inf
     return n
 
 
