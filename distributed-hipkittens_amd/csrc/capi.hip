@@ -789,8 +789,10 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
                             int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
                             int32_t inter, int scale_mode, int w_layout, void* out, void* workspace,
                             size_t workspace_bytes, hkmoe_stream_t stream, bool aux_ok) {
-  HK_REQUIRE(x_q && x_scale && logits && w13 && w13_scale && w2 && w2_scale && out,
-             "moe_forward: null pointer");
+  // with no tokens the activations, the output and the workspace may be empty
+  // (null); the weights and shapes are checked either way
+  HK_REQUIRE(w13 && w13_scale && w2 && w2_scale, "moe_forward: null pointer");
+  HK_REQUIRE(num_tokens == 0 || (x_q && x_scale && logits && out), "moe_forward: null pointer");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
              "moe_forward: bad scale_mode %d", scale_mode);
   HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "moe_forward: bad w_layout %d",
@@ -802,13 +804,13 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0 && hidden <= kGroup * kMaxKBlocks,
              "moe_forward: hidden=%d must be a multiple of 256 and <= %d", hidden, kGroup * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "moe_forward: inter=%d must be a multiple of 128", inter);
+  if (num_tokens == 0) return HKMOE_OK;
   const bool block = scale_mode == HKMOE_SCALE_BLOCK;
   const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, scale_mode);
   if (workspace == nullptr || workspace_bytes < need.bytes)
     return fail(HKMOE_ERR_WORKSPACE, "moe_forward: workspace of %zu bytes needed, %zu given", need.bytes,
                 workspace_bytes);
   HK_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "moe_forward: workspace must be 256-byte aligned");
-  if (num_tokens == 0) return HKMOE_OK;
   const MoeWorkspace w = carve(static_cast<uint8_t*>(workspace), num_tokens, num_experts, top_k,
                                hidden, inter, scale_mode);
   const int64_t rows = num_tokens * top_k;
@@ -1155,7 +1157,9 @@ int hkmoe_moe_forward_mx(const void* x_q, const void* x_e8m0, const float* logit
                          const void* w13_words, const void* w2, const void* w2_words, int64_t num_tokens,
                          int32_t num_experts, int32_t top_k, int32_t hidden, int32_t inter, int w_layout,
                          void* out, void* workspace, size_t workspace_bytes, hkmoe_stream_t stream) {
-  HK_REQUIRE(x_q && x_e8m0 && logits && w13 && w13_words && w2 && w2_words && out, "moe_forward_mx: null pointer");
+  // with no tokens the activations, the output and the workspace may be empty (null)
+  HK_REQUIRE(w13 && w13_words && w2 && w2_words, "moe_forward_mx: null pointer");
+  HK_REQUIRE(num_tokens == 0 || (x_q && x_e8m0 && logits && out), "moe_forward_mx: null pointer");
   HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "moe_forward_mx: bad w_layout %d",
              w_layout);
   HK_REQUIRE(num_tokens >= 0 && num_tokens * top_k < (1ll << 31), "moe_forward_mx: bad T");
@@ -1166,12 +1170,12 @@ int hkmoe_moe_forward_mx(const void* x_q, const void* x_e8m0, const float* logit
              "moe_forward_mx: hidden=%d must be a multiple of 256 and <= %d", hidden, kGroup * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0 && inter <= kGroup * kMaxKBlocks,
              "moe_forward_mx: inter=%d must be a multiple of 128 and <= %d", inter, kGroup * kMaxKBlocks);
+  if (num_tokens == 0) return HKMOE_OK;
   const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, HKMOE_SCALE_MX);
   if (workspace == nullptr || workspace_bytes < need.bytes)
     return fail(HKMOE_ERR_WORKSPACE, "moe_forward_mx: workspace of %zu bytes needed, %zu given", need.bytes,
                 workspace_bytes);
   HK_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "moe_forward_mx: workspace must be 256-byte aligned");
-  if (num_tokens == 0) return HKMOE_OK;
   const MoeWorkspace w = carve(static_cast<uint8_t*>(workspace), num_tokens, num_experts, top_k, hidden,
                                inter, HKMOE_SCALE_MX);
   const int64_t rows = num_tokens * top_k;

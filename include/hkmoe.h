@@ -259,6 +259,9 @@ int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, i
  *   256-byte aligned, holding every intermediate (routing, permutation, h, y).
  *   hkmoe_moe_workspace_size also sizes hkmoe_moe_forward_mx's workspace with
  *   scale_mode HKMOE_SCALE_MX (0 for an unknown mode).
+ *   T == 0: weights and shapes are checked, nothing is launched, and x_q,
+ *   x_scale (block), logits, out and the workspace may be null (the same for
+ *   hkmoe_moe_forward_mx and hkmoe_moe_forward_noalloc).
  */
 size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t top_k,
                                 int32_t hidden, int32_t inter, int scale_mode);

@@ -88,6 +88,31 @@ def test_moe_forward_argument_errors(lib):
     assert "hidden=4000" in _err(lib)
 
 
+def test_moe_forward_empty_batch(lib):
+    """T = 0: nothing is launched (no GPU needed); activations, output and
+    workspace may be null, the weights and shapes are still checked."""
+    fake = ctypes.c_void_p(0x1000)
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    shape = [i64(0), i32(8), i32(2), i32(4096), i32(1024)]
+    args = [None, None, None, fake, fake, fake, fake] + shape + [1, 0, None, None, ctypes.c_size_t(0), None]
+    assert lib.hkmoe_moe_forward(*args) == 0
+    noalloc = [None, None, None, fake, fake, fake, fake] + shape + [1, 0, None, None]
+    assert lib.hkmoe_moe_forward_noalloc(*noalloc) == 0
+    mx = [None, None, None, fake, fake, fake, fake] + shape + [1, None, None, ctypes.c_size_t(0), None]
+    assert lib.hkmoe_moe_forward_mx(*mx) == 0
+    args[3] = None  # the weights are still required
+    assert lib.hkmoe_moe_forward(*args) == 1
+    assert "null pointer" in _err(lib)
+    args[3] = fake
+    args[10] = i32(4000)  # and the shapes checked
+    assert lib.hkmoe_moe_forward(*args) == 1
+    assert "hidden=4000" in _err(lib)
+    args[10] = i32(4096)
+    args[7] = i64(64)  # with tokens, null activations are an error
+    assert lib.hkmoe_moe_forward(*args) == 1
+    assert "null pointer" in _err(lib)
+
+
 def test_grouped_gemm_format_errors(lib):
     fake = ctypes.c_void_p(0x1000)
     i64, i32 = ctypes.c_int64, ctypes.c_int32

@@ -119,6 +119,28 @@ def test_moe_single_call_matches_steps(hk, name):
     assert torch.equal(o1.view(torch.int16), out.view(torch.int16))
 
 
+@pytest.mark.parametrize("name", ["tensor_e8k2", "block_e16k4_skew"])
+def test_moe_empty_batch(hk, name):
+    """T = 0 tokens: the layer returns an empty [0, H] output and launches nothing
+    that fails; the same layer then still matches the stepwise path."""
+    d = synth.make_moe(seed=13, **SMALL[name])
+    g = moe_inputs_to_gpu(d)
+    layer = hk.MoELayer(g["w13_q"], g["w13_scale"], g["w2_q"], g["w2_scale"], g["top_k"])
+    hdim = g["x_q"].shape[1]
+    x0 = g["x_q"][:0]
+    s0 = g["x_scale"][:, :0] if g["x_scale"].dim() == 2 else g["x_scale"]
+    out0 = layer(x0, s0, g["logits"][:0])
+    torch.cuda.synchronize()
+    assert tuple(out0.shape) == (0, hdim) and out0.dtype == torch.bfloat16
+    out = layer(g["x_q"], g["x_scale"], g["logits"])
+    r = _run_steps(hk, g, keep_h=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), r["out"].view(torch.int16))
+    out0 = layer(x0, s0, g["logits"][:0])
+    torch.cuda.synchronize()
+    assert tuple(out0.shape) == (0, hdim)
+
+
 @pytest.mark.parametrize("name", ["tensor_e8k2", "block_e16k4_skew", "block_e64k8_skew", "tensor_e5k5"])
 def test_packed_weights_bit_exact(hk, name):
     """Grouped GEMMs on hkmoe_pack_weights output == on row-major weights, bit
