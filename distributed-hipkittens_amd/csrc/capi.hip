@@ -309,7 +309,7 @@ const char* hkmoe_last_error(void) { return g_last_error.c_str(); }
 
 int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
                    const float* scale_a, const float* scale_b, int out_dtype, hkmoe_stream_t stream) {
-  HK_REQUIRE(a && b && c, "gemm_fp8: null tensor pointer");
+  HK_REQUIRE(b && (m == 0 || (a && c)), "gemm_fp8: null tensor pointer");
   HK_REQUIRE(m >= 0 && n > 0 && k > 0, "gemm_fp8: bad shape M=%lld N=%lld K=%lld", (long long)m,
              (long long)n, (long long)k);
   HK_REQUIRE(k % 128 == 0, "gemm_fp8: K=%lld must be a multiple of 128", (long long)k);
@@ -359,7 +359,7 @@ int hkmoe_route_blocks(int64_t num_tokens) { return route_blocks(num_tokens); }
 
 int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_experts, int32_t top_k,
                      int32_t* topk_idx, float* topk_w, int32_t* block_counts, hkmoe_stream_t stream) {
-  HK_REQUIRE(logits && topk_idx && topk_w && block_counts, "route_topk: null pointer");
+  HK_REQUIRE(num_tokens == 0 || (logits && topk_idx && topk_w && block_counts), "route_topk: null pointer");
   HK_REQUIRE(num_tokens >= 0 && num_tokens < (1ll << 31) / kMaxTopK, "route_topk: bad T=%lld",
              (long long)num_tokens);
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "route_topk: E=%d outside [1, %d]",
@@ -382,7 +382,7 @@ int hkmoe_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32_
                          int32_t* counts, int32_t* offsets, int32_t* block_base,
                          int32_t* mtile_offsets, int32_t* mtile_list, float* amax_reset,
                          int32_t* tile_counters, hkmoe_stream_t stream) {
-  HK_REQUIRE(counts && offsets && block_base && mtile_offsets, "expert_offsets: null pointer");
+  HK_REQUIRE(counts && offsets && mtile_offsets && (num_tokens == 0 || block_base), "expert_offsets: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "expert_offsets: E=%d outside [1, %d]",
              num_experts, kMaxExperts);
   HK_REQUIRE(num_tokens >= 0, "expert_offsets: bad T");
@@ -397,7 +397,7 @@ int hkmoe_expert_offsets_narrow(const int32_t* block_counts, int64_t num_tokens,
                                 int32_t* mtile_offsets, int32_t* mtile_list, float* amax_reset,
                                 int32_t* tile_counters, int32_t narrow_max, int32_t* narrow_info,
                                 hkmoe_stream_t stream) {
-  HK_REQUIRE(counts && offsets && block_base && mtile_offsets && mtile_list && narrow_info,
+  HK_REQUIRE(counts && offsets && mtile_offsets && mtile_list && narrow_info && (num_tokens == 0 || block_base),
              "expert_offsets_narrow: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "expert_offsets_narrow: E=%d outside [1, %d]",
              num_experts, kMaxExperts);
@@ -414,7 +414,7 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
                   const int32_t* offsets, const int32_t* block_base, int32_t* perm, int32_t* inv_perm,
                   const void* x_q, const float* x_scale, int64_t hidden, int scale_mode, void* xp,
                   float* xp_scale_t, hkmoe_stream_t stream) {
-  HK_REQUIRE(topk_idx && offsets && block_base && perm && inv_perm, "scatter: null pointer");
+  HK_REQUIRE(num_tokens == 0 || (topk_idx && offsets && block_base && perm && inv_perm), "scatter: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "scatter: E=%d outside [1, %d]",
              num_experts, kMaxExperts);
   HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK, "scatter: bad top_k=%d", top_k);
@@ -453,14 +453,14 @@ static int grouped_gemm1_impl(const void* x, const float* x_scale, const int32_t
                               int32_t* tile_counters, hkmoe_stream_t stream,
                               const int32_t* narrow_cnt, int yield_from, int narrow_active,
                               int narrow_grid = 0) {
-  HK_REQUIRE(x && w13 && offsets && mtile_offsets && h, "grouped_gemm1: null pointer");
-  HK_REQUIRE(x_scale && w13_scale, "grouped_gemm1: null scale pointer");
+  HK_REQUIRE(w13 && w13_scale && offsets && mtile_offsets, "grouped_gemm1: null pointer");
+  HK_REQUIRE(rows == 0 || (x && x_scale && h), "grouped_gemm1: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kGroup == 0 && hidden <= kGroup * kMaxKBlocks,
              "grouped_gemm1: hidden=%d must be a multiple of 128 and <= %d", hidden, kGroup * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "grouped_gemm1: inter=%d must be a multiple of 128", inter);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm1: bad rows");
-  HK_REQUIRE(x_rows >= 1 && x_rows * hidden < (1ll << 32), "grouped_gemm1: x_rows=%lld out of range",
+  HK_REQUIRE(x_rows >= (rows > 0 ? 1 : 0) && x_rows * hidden < (1ll << 32), "grouped_gemm1: x_rows=%lld out of range",
              (long long)x_rows);
   HK_REQUIRE(gather == nullptr || gather_div >= 1, "grouped_gemm1: gather_div must be >= 1");
   HK_REQUIRE(gather != nullptr || x_rows >= rows, "grouped_gemm1: x has fewer rows than rows");
@@ -471,7 +471,7 @@ static int grouped_gemm1_impl(const void* x, const float* x_scale, const int32_t
              w_layout);
   HK_REQUIRE(out_format == HKMOE_BF16 || (out_format == HKMOE_E4M3 && scale_mode == HKMOE_SCALE_BLOCK),
              "grouped_gemm1: out_format %d not supported with scale_mode %d", out_format, scale_mode);
-  HK_REQUIRE(out_format != HKMOE_E4M3 || h_aux != nullptr, "grouped_gemm1: e4m3 output needs h_aux scales");
+  HK_REQUIRE(out_format != HKMOE_E4M3 || rows == 0 || h_aux != nullptr, "grouped_gemm1: e4m3 output needs h_aux scales");
   if (rows == 0) return HKMOE_OK;
   GemmParams p{};
   p.a = static_cast<const uint8_t*>(x);
@@ -533,9 +533,11 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
 
 int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, const float* amax,
                   void* hq, float* hs, hkmoe_stream_t stream) {
-  HK_REQUIRE(h && hq && hs, "requant: null pointer");
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "requant: inter=%d must be a multiple of 128", inter);
   HK_REQUIRE(rows >= 0, "requant: bad rows");
+  // rows == 0: h and hq are empty; block scales hs too, a tensor scale is still written
+  HK_REQUIRE(rows == 0 || (h && hq), "requant: null pointer");
+  HK_REQUIRE(hs || (rows == 0 && scale_mode == HKMOE_SCALE_BLOCK), "requant: null pointer");
   auto s = static_cast<hipStream_t>(stream);
   if (scale_mode == HKMOE_SCALE_BLOCK) {
     if (rows == 0) return HKMOE_OK;
@@ -560,7 +562,8 @@ static int grouped_gemm2_impl(const void* hq, const float* hs, const void* w2, c
                               int w_layout, void* y, int32_t* tile_counters, hkmoe_stream_t stream,
                               const int32_t* narrow_cnt, int yield_from, int narrow_active,
                               int narrow_grid = 0) {
-  HK_REQUIRE(hq && hs && w2 && w2_scale && offsets && mtile_offsets && y, "grouped_gemm2: null pointer");
+  HK_REQUIRE(w2 && w2_scale && offsets && mtile_offsets, "grouped_gemm2: null pointer");
+  HK_REQUIRE(rows == 0 || (hq && hs && y), "grouped_gemm2: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2: hidden=%d must be a multiple of 256", hidden);
   HK_REQUIRE(inter > 0 && inter % kGroup == 0 && inter <= kGroup * kMaxKBlocks,
@@ -686,7 +689,7 @@ int hkmoe_requant_quotient_check(int32_t* counts, hkmoe_stream_t stream) {
 
 int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, int64_t num_tokens,
                   int32_t top_k, int32_t hidden, void* out, hkmoe_stream_t stream) {
-  HK_REQUIRE(y && topk_w && inv_perm && out, "combine: null pointer");
+  HK_REQUIRE(num_tokens == 0 || (y && topk_w && inv_perm && out), "combine: null pointer");
   HK_REQUIRE(top_k >= 1 && top_k <= kMaxTopK, "combine: bad top_k=%d", top_k);
   HK_REQUIRE(hidden > 0 && hidden % 8 == 0, "combine: hidden=%d must be a multiple of 8", hidden);
   HK_REQUIRE(num_tokens >= 0 && num_tokens < (1ll << 31), "combine: bad T");
@@ -918,7 +921,7 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
 // ---------------------------------------------------------------------------
 int hkmoe_quant_group(const float* x, int64_t rows, int64_t cols, void* q, float* s,
                       hkmoe_stream_t stream) {
-  HK_REQUIRE(x && q && s, "quant_group: null pointer");
+  HK_REQUIRE(rows == 0 || (x && q && s), "quant_group: null pointer");
   HK_REQUIRE(rows >= 0 && cols > 0 && cols % kGroup == 0, "quant_group: cols must be a multiple of 128");
   const int64_t waves = rows * (cols / kGroup);
   if (waves == 0) return HKMOE_OK;
@@ -930,7 +933,7 @@ int hkmoe_quant_group(const float* x, int64_t rows, int64_t cols, void* q, float
 
 int hkmoe_quant_block(const float* x, int64_t batch, int64_t rows, int64_t cols, void* q, float* s,
                       hkmoe_stream_t stream) {
-  HK_REQUIRE(x && q && s, "quant_block: null pointer");
+  HK_REQUIRE(batch == 0 || (x && q && s), "quant_block: null pointer");
   HK_REQUIRE(batch >= 0 && rows > 0 && cols > 0 && rows % kGroup == 0 && cols % kGroup == 0,
              "quant_block: rows and cols must be multiples of 128");
   const int64_t blocks = batch * (rows / kGroup) * (cols / kGroup);
@@ -943,7 +946,7 @@ int hkmoe_quant_block(const float* x, int64_t batch, int64_t rows, int64_t cols,
 
 int hkmoe_quant_tensor(const float* x, int64_t rows, int64_t cols, void* q, float* s, float* amax_ws,
                        hkmoe_stream_t stream) {
-  HK_REQUIRE(x && q && s && amax_ws, "quant_tensor: null pointer");
+  HK_REQUIRE(s && amax_ws && (rows == 0 || cols == 0 || (x && q)), "quant_tensor: null pointer");
   HK_REQUIRE(rows >= 0 && cols >= 0, "quant_tensor: bad shape");
   const int64_t n = rows * cols;
   auto st = static_cast<hipStream_t>(stream);
@@ -963,7 +966,7 @@ int hkmoe_quant_tensor(const float* x, int64_t rows, int64_t cols, void* q, floa
 // MX (e8m0 1x32) operands and GEMM
 // ---------------------------------------------------------------------------
 int hkmoe_quant_mx(const float* x, int64_t rows, int64_t cols, void* q, void* s, hkmoe_stream_t stream) {
-  HK_REQUIRE(x && q && s, "quant_mx: null pointer");
+  HK_REQUIRE(rows == 0 || (x && q && s), "quant_mx: null pointer");
   HK_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, "quant_mx: cols=%lld must be a positive multiple of 32",
              (long long)cols);
   const int64_t blocks = rows * (cols / 32);
@@ -975,7 +978,7 @@ int hkmoe_quant_mx(const float* x, int64_t rows, int64_t cols, void* q, void* s,
 }
 
 int hkmoe_mx_pack_scales(const void* s, int64_t rows, int64_t cols, void* packed, hkmoe_stream_t stream) {
-  HK_REQUIRE(s && packed, "mx_pack_scales: null pointer");
+  HK_REQUIRE(rows == 0 || (s && packed), "mx_pack_scales: null pointer");
   HK_REQUIRE(rows >= 0 && cols > 0 && cols % kBK == 0,
              "mx_pack_scales: cols=%lld must be a positive multiple of 128", (long long)cols);
   const int64_t rows64 = (rows + 63) / 64 * 64;
@@ -990,7 +993,7 @@ int hkmoe_mx_pack_scales(const void* s, int64_t rows, int64_t cols, void* packed
 
 int hkmoe_gemm_mx(const void* a, const void* a_scale, const void* b, const void* b_scale, void* c, int64_t m,
                   int64_t n, int64_t k, int out_dtype, hkmoe_stream_t stream) {
-  HK_REQUIRE(a && a_scale && b && b_scale && c, "gemm_mx: null pointer");
+  HK_REQUIRE(b && b_scale && (m == 0 || (a && a_scale && c)), "gemm_mx: null pointer");
   HK_REQUIRE(m >= 0 && n > 0 && k > 0, "gemm_mx: bad shape M=%lld N=%lld K=%lld", (long long)m, (long long)n,
              (long long)k);
   HK_REQUIRE(k % kBK == 0, "gemm_mx: K=%lld must be a multiple of 128", (long long)k);
@@ -1047,7 +1050,8 @@ int hkmoe_mx_pack_weight_scales(const void* s, int64_t num_experts, int64_t n, i
 int hkmoe_mx_gather_scales(const void* s, int64_t x_rows, int32_t k, const int32_t* gather, int32_t gather_div,
                            const int32_t* offsets, const int32_t* mtile_offsets, int32_t num_experts,
                            int64_t rows, void* words, hkmoe_stream_t stream) {
-  HK_REQUIRE(s && offsets && mtile_offsets && words, "mx_gather_scales: null pointer");
+  HK_REQUIRE(offsets && mtile_offsets, "mx_gather_scales: null pointer");
+  HK_REQUIRE(rows == 0 || (s && words), "mx_gather_scales: null pointer");
   HK_REQUIRE(k > 0 && k % kBK == 0, "mx_gather_scales: K=%d must be a multiple of 128", k);
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "mx_gather_scales: bad E=%d", num_experts);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31) && x_rows >= 0, "mx_gather_scales: bad rows");
@@ -1066,13 +1070,14 @@ int hkmoe_grouped_gemm1_mx(const void* x, const void* x_words, const int32_t* ga
                            const int32_t* mtile_offsets, const int32_t* mtile_list, int64_t rows,
                            int32_t num_experts, int32_t hidden, int32_t inter, int w_layout, int out_format,
                            void* h, void* h_words, int32_t* tile_counters, hkmoe_stream_t stream) {
-  HK_REQUIRE(x && x_words && w13 && w13_words && offsets && mtile_offsets && h, "grouped_gemm1_mx: null pointer");
+  HK_REQUIRE(w13 && w13_words && offsets && mtile_offsets, "grouped_gemm1_mx: null pointer");
+  HK_REQUIRE(rows == 0 || (x && x_words && h), "grouped_gemm1_mx: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm1_mx: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kGroup == 0 && hidden <= kGroup * kMaxKBlocks,
              "grouped_gemm1_mx: hidden=%d must be a multiple of 128 and <= %d", hidden, kGroup * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0, "grouped_gemm1_mx: inter=%d must be a multiple of 128", inter);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm1_mx: bad rows");
-  HK_REQUIRE(x_rows >= 1 && x_rows * hidden < (1ll << 32), "grouped_gemm1_mx: x_rows=%lld out of range",
+  HK_REQUIRE(x_rows >= (rows > 0 ? 1 : 0) && x_rows * hidden < (1ll << 32), "grouped_gemm1_mx: x_rows=%lld out of range",
              (long long)x_rows);
   HK_REQUIRE(gather == nullptr || gather_div >= 1, "grouped_gemm1_mx: gather_div must be >= 1");
   HK_REQUIRE(gather != nullptr || x_rows >= rows, "grouped_gemm1_mx: x has fewer rows than rows");
@@ -1118,7 +1123,8 @@ int hkmoe_grouped_gemm2_mx(const void* hq, const void* hq_words, const void* w2,
                            const int32_t* offsets, const int32_t* mtile_offsets, const int32_t* mtile_list,
                            int64_t rows, int32_t num_experts, int32_t hidden, int32_t inter, int w_layout,
                            void* y, int32_t* tile_counters, hkmoe_stream_t stream) {
-  HK_REQUIRE(hq && hq_words && w2 && w2_words && offsets && mtile_offsets && y, "grouped_gemm2_mx: null pointer");
+  HK_REQUIRE(w2 && w2_words && offsets && mtile_offsets, "grouped_gemm2_mx: null pointer");
+  HK_REQUIRE(rows == 0 || (hq && hq_words && y), "grouped_gemm2_mx: null pointer");
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "grouped_gemm2_mx: bad E=%d", num_experts);
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0, "grouped_gemm2_mx: hidden=%d must be a multiple of 256", hidden);
   HK_REQUIRE(inter > 0 && inter % kGroup == 0 && inter <= kGroup * kMaxKBlocks,

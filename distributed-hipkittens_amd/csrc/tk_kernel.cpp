@@ -204,10 +204,10 @@ void dispatch_scatter(py::object idx, py::object offsets, py::object block_base,
     want_dim(x, "x_q", 2);
     hidden = x.shape[1];
     if (x.shape[0] != t) throw std::runtime_error("x_q must be [T, H]");
-    if (!d.ptr || d.numel() != t * k * hidden) throw std::runtime_error("xp must be [T*k, H]");
+    if ((t > 0 && !d.ptr) || d.numel() != t * k * hidden) throw std::runtime_error("xp must be [T*k, H]");
     if (ds.ptr) {
       mode = HKMOE_SCALE_BLOCK;
-      if (!xs.ptr || xs.numel() != t * (hidden / 128) || ds.numel() != t * k * (hidden / 128))
+      if ((t > 0 && !xs.ptr) || xs.numel() != t * (hidden / 128) || ds.numel() != t * k * (hidden / 128))
         throw std::runtime_error("block scales: x_scale [T, H/128], xp_scale_t [H/128, T*k]");
     }
   }
@@ -257,7 +257,7 @@ void dispatch_grouped_gemm1(py::object x_q, py::object x_scale, py::object gathe
   if (mode == HKMOE_SCALE_BLOCK &&
       (xs.numel() != x_rows * (hidden / 128) || ws.numel() != e * (2 * inter / 128) * (hidden / 128)))
     throw std::runtime_error("block scales: x_scale [x_rows, H/128], w13_scale [E, 2I/128, H/128]");
-  if (fmt == HKMOE_E4M3 && (!aux.ptr || aux.numel() != rows * (inter / 128)))
+  if (fmt == HKMOE_E4M3 && ((rows > 0 && !aux.ptr) || aux.numel() != rows * (inter / 128)))
     throw std::runtime_error("e4m3 output needs h_aux [I/128, rows] group scales");
   if (ni.ptr) {
     if (mode != HKMOE_SCALE_BLOCK || fmt != HKMOE_E4M3 || !ml.ptr)
@@ -581,7 +581,7 @@ void dispatch_grouped_gemm1_mx(py::object x_q, py::object x_words, py::object ga
   if (hh.dtype == kBf16) fmt = HKMOE_BF16;
   else if (hh.dtype == kF8) fmt = HKMOE_E4M3;
   else throw std::runtime_error("h: expected bfloat16 or float8_e4m3fn");
-  if (fmt == HKMOE_E4M3 && (!hw.ptr || hw.numel() != (inter / 128) * mx_ws(rows, e)))
+  if (fmt == HKMOE_E4M3 && ((rows > 0 && !hw.ptr) || hw.numel() != (inter / 128) * mx_ws(rows, e)))
     throw std::runtime_error("e4m3 output needs h_words [I/128, ws]");
   check(hkmoe_grouped_gemm1_mx(x.ptr, xw.ptr, static_cast<const int32_t*>(gth.ptr), gather_div, x_rows, w.ptr,
                                ww.ptr, static_cast<const int32_t*>(o.ptr), static_cast<const int32_t*>(mo.ptr),

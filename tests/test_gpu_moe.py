@@ -139,6 +139,28 @@ def test_moe_empty_batch(hk, name):
     out0 = layer(x0, s0, g["logits"][:0])
     torch.cuda.synchronize()
     assert tuple(out0.shape) == (0, hdim)
+    # the stepwise path (routing, scatter, both grouped GEMMs, combine) on no rows
+    r0 = hk.moe_forward_steps(x0, s0, g["logits"][:0], g["w13_q"], g["w13_scale"], g["w2_q"],
+                              g["w2_scale"], g["top_k"])
+    torch.cuda.synchronize()
+    assert tuple(r0["out"].shape) == (0, hdim)
+
+
+def test_empty_dense_and_quantisers(hk):
+    """M = 0 / no rows: the dense GEMMs and the quantisers return empty results."""
+    a = torch.empty((0, 256), dtype=torch.float32, device="cuda")
+    b = torch.randn((256, 256), device="cuda")
+    aq, sa = hk.quant_tensor(a)
+    bq, sb = hk.quant_tensor(b)
+    c = hk.gemm_fp8(aq, bq, sa, sb)
+    gq, gs = hk.quant_group(a)
+    mq, ms = hk.quant_mx(a)
+    bmq, bms = hk.quant_mx(b)
+    cm = hk.gemm_mx(mq, hk.mx_pack_scales(ms), bmq, hk.mx_pack_scales(bms))
+    torch.cuda.synchronize()
+    assert tuple(c.shape) == (0, 256) and tuple(cm.shape) == (0, 256)
+    assert aq.numel() == 0 and gq.numel() == 0 and mq.numel() == 0 and gs.numel() == 0
+    assert torch.isfinite(sa).all()
 
 
 @pytest.mark.parametrize("name", ["tensor_e8k2", "block_e16k4_skew", "block_e64k8_skew", "tensor_e5k5"])
