@@ -822,19 +822,45 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
   // the weight-streaming narrow kernels on an auxiliary stream, which run
   // beside the 256x256 kernels of the larger experts on the main stream.
   const NarrowConfig nc = narrow_config();
+  const bool narrow_ok = aux_ok && block && nc.cus > 0 && nc.max_rows > 0 && narrow_depth(hidden / kBK) > 0 &&
+                         narrow_depth(inter / kBK) > 0;
+  // Decode-like shapes (T*k <= E*max_rows: mostly or only narrow experts): the
+  // narrow kernels run on `stream` after the 256x256 ones, each on every CU,
+  // without the fork to the auxiliary stream and the join back (together
+  // ≈20 µs of cross-stream latency on the critical path of a 0.5 ms layer).
+  const bool narrow_seq = narrow_ok && rows <= static_cast<int64_t>(num_experts) * nc.max_rows;
   AuxStreams* aux = nullptr;
-  if (aux_ok && block && nc.cus > 0 && nc.max_rows > 0 && narrow_depth(hidden / kBK) > 0 &&
-      narrow_depth(inter / kBK) > 0)
-    HK_TRY(get_aux(s, &aux));
+  if (narrow_ok && !narrow_seq) HK_TRY(get_aux(s, &aux));
   std::unique_lock<std::mutex> aux_lock(g_aux_mu, std::defer_lock);
   if (aux) aux_lock.lock();
   HK_TRY(hkmoe_route_topk(logits, num_tokens, num_experts, top_k, w.topk_idx, w.topk_w,
                           w.block_counts, stream));
   HK_TRY(launch_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets,
                                w.block_base, w.mtile_offsets, w.mtile_list, w.amax, w.tile_ctr,
-                               aux ? nc.max_rows : 0, aux ? w.narrow_info : nullptr, s));
+                               (aux || narrow_seq) ? nc.max_rows : 0,
+                               (aux || narrow_seq) ? w.narrow_info : nullptr, s));
   HK_TRY(hkmoe_scatter(w.topk_idx, num_tokens, num_experts, top_k, w.offsets, w.block_base, w.perm,
                        w.inv_perm, nullptr, nullptr, hidden, scale_mode, nullptr, nullptr, stream));
+  if (narrow_seq) {
+    // one stream: each 256x256 GEMM keeps every CU (yield_from 0) and skips the
+    // narrow experts' tiles; each narrow GEMM then runs its items on every CU
+    const int ngrid = device_cus();
+    HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
+                              w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
+                              w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream, w.narrow_info, 0, 0));
+    HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
+                              w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
+                              w_layout, HKMOE_E4M3, w.hq, w.hs, w.narrow_info + 1, stream, w.narrow_info, 0,
+                              ngrid, ngrid));
+    HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
+                              num_experts, hidden, inter, scale_mode, w_layout, w.y, w.tile_ctr + 8, stream,
+                              w.narrow_info, 0, 0));
+    HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
+                              num_experts, hidden, inter, scale_mode, w_layout, w.y, w.narrow_info + 2, stream,
+                              w.narrow_info, 0, ngrid, ngrid));
+    HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
+    return HKMOE_OK;
+  }
   if (aux) {
     // fork: both GEMMs of the narrow experts on the auxiliary stream, enqueued
     // first so that their workgroups find free CUs; join before the combine
@@ -862,9 +888,8 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
     // share == 2: once the narrow GEMMs are done, their CUs join the first 256x256
     // GEMM's tile queues (a second launch of it on the auxiliary stream, which
     // takes whatever tiles are left); the second 256x256 GEMM then waits for both.
-    // Not when every row fits narrow experts (rows <= E * max_rows, decode-like):
-    // there the extra launch would only lengthen the critical path.
-    const bool late_join = nc.share == 2 && rows > static_cast<int64_t>(num_experts) * nc.max_rows;
+    // (Decode-like shapes, rows <= E * max_rows, took the one-stream path above.)
+    const bool late_join = nc.share == 2;
     if (late_join)
       HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                                 w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,

@@ -277,8 +277,9 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
  * wide_share 1 or 2 runs the first wide GEMM on (CUs - cus) workgroups while
  * narrow experts exist; with 2 the narrow path's CUs also join that GEMM's
  * remaining tiles once both narrow GEMMs are done (a second launch of it on the
- * auxiliary stream), and the second wide GEMM waits for them; this late join is
- * skipped when T*top_k <= E*max_rows.  Other values are rejected.
+ * auxiliary stream), and the second wide GEMM waits for them.  Other values are
+ * rejected.  Decode-like shapes (T*top_k <= E*max_rows) use no auxiliary stream:
+ * each narrow GEMM runs on the caller's stream after the wide one, on every CU.
  * It also stays off when H/128 or I/128 is odd or above 64, and for a first call made
  * while the caller's stream is being captured into a graph (the auxiliary
  * stream is created on the first call that is not captured).  Defaults come
