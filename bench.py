@@ -559,8 +559,10 @@ def _write_timeline(f, path, n_calls):
     i0 = starts[n_calls - 1]
     i1 = starts[n_calls] if len(starts) > n_calls else len(ks)
     t0 = int(ks[i0]["Start_Timestamp"])
-    f.write("\nTimeline of the last timed layer call (one `MoELayer` call: the narrow kernels run on the "
-            "library's auxiliary stream beside the 256x256 GEMMs):\n\n")
+    f.write("\nTimeline of the last timed layer call (one `MoELayer` call: with block scales the narrow "
+            "kernels run on the library's auxiliary stream beside the 256x256 GEMMs, or, for decode-like "
+            "shapes with T*k <= E*64, on the same stream after each of them; per-tensor layers have no "
+            "narrow kernels):\n\n")
     f.write("| kernel | start us | end us | duration us |\n|---|---|---|---|\n")
     for r in ks[i0:i1]:
         lab = _kernel_label(r["Kernel_Name"], False)
