@@ -824,11 +824,14 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
   const NarrowConfig nc = narrow_config();
   const bool narrow_ok = aux_ok && block && nc.cus > 0 && nc.max_rows > 0 && narrow_depth(hidden / kBK) > 0 &&
                          narrow_depth(inter / kBK) > 0;
-  // Decode-like shapes (T*k <= E*max_rows: mostly or only narrow experts): the
-  // narrow kernels run on `stream` after the 256x256 ones, each on every CU,
-  // without the fork to the auxiliary stream and the join back (together
-  // ≈20 µs of cross-stream latency on the critical path of a 0.5 ms layer).
-  const bool narrow_seq = narrow_ok && rows <= static_cast<int64_t>(num_experts) * nc.max_rows;
+  // Up to 2*max_rows rows per expert on average (T*k <= 2*E*max_rows) the small
+  // experts' weight stream dominates: the narrow kernels then run on `stream`
+  // after the 256x256 ones, each on every CU, instead of on max. 3/4 of them
+  // beside the 256x256 kernels, and without the fork to the auxiliary stream and
+  // the join back (≈20 µs of cross-stream latency).  Measured on the config-3
+  // shape (H=7168, I=2048, E=256, k=8): T=512 / 1024 / 2048 / 4096 run 26 / 21 /
+  // 13 / 4% faster on one stream, T=6144 / 8192 10 / 8% slower.
+  const bool narrow_seq = narrow_ok && rows <= 2 * static_cast<int64_t>(num_experts) * nc.max_rows;
   AuxStreams* aux = nullptr;
   if (narrow_ok && !narrow_seq) HK_TRY(get_aux(s, &aux));
   std::unique_lock<std::mutex> aux_lock(g_aux_mu, std::defer_lock);
@@ -888,7 +891,7 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
     // share == 2: once the narrow GEMMs are done, their CUs join the first 256x256
     // GEMM's tile queues (a second launch of it on the auxiliary stream, which
     // takes whatever tiles are left); the second 256x256 GEMM then waits for both.
-    // (Decode-like shapes, rows <= E * max_rows, took the one-stream path above.)
+    // (Shapes with rows <= 2 * E * max_rows took the one-stream path above.)
     const bool late_join = nc.share == 2;
     if (late_join)
       HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,

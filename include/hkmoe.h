@@ -278,8 +278,9 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
  * narrow experts exist; with 2 the narrow path's CUs also join that GEMM's
  * remaining tiles once both narrow GEMMs are done (a second launch of it on the
  * auxiliary stream), and the second wide GEMM waits for them.  Other values are
- * rejected.  Decode-like shapes (T*top_k <= E*max_rows) use no auxiliary stream:
- * each narrow GEMM runs on the caller's stream after the wide one, on every CU.
+ * rejected.  Shapes with T*top_k <= 2*E*max_rows (small experts dominate) use
+ * no auxiliary stream: each narrow GEMM runs on the caller's stream after the
+ * wide one, on every CU (and wide_share does not apply).
  * It also stays off when H/128 or I/128 is odd or above 64, and for a first call made
  * while the caller's stream is being captured into a graph (the auxiliary
  * stream is created on the first call that is not captured).  Defaults come

@@ -14,7 +14,8 @@ other inputs) and synchronises, and that eager result is checked as well.
 The narrow path (block scales, even H/128 and I/128) forks to the library's
 auxiliary stream and joins back through events; under capture the auxiliary
 stream joins the graph the same way, with the late join (wide_share 2) and
-without it (1).
+without it (1).  Where T*k <= 2*E*max_rows it stays on the caller's stream,
+which the capture takes as it is.
 """
 import pytest
 import torch
@@ -109,14 +110,16 @@ def test_moe_layer_mx_graph_replay(hk):
     _replay_and_check(layer, sets)
 
 
-@pytest.mark.parametrize("share", [1, 2])
-def test_moe_layer_graph_replay_narrow(hk, share):
-    """Block-scaled layer with experts of both kinds (<= 32 rows: narrow kernel;
-    larger: 256x256) captured with the narrow path on."""
+@pytest.mark.parametrize("share,max_rows", [(1, 16), (2, 16), (1, 32)])
+def test_moe_layer_graph_replay_narrow(hk, share, max_rows):
+    """Block-scaled layer with experts of both kinds (<= max_rows rows: narrow
+    kernel; larger: 256x256) captured with the narrow path on.  T*k = 1200:
+    above 2*E*16 = 1024 the narrow kernels run on the auxiliary stream (with
+    share 2 also the late join), at or below 2*E*32 = 2048 on the caller's
+    stream after the 256x256 ones."""
     t, h, i, e, k = 300, 512, 256, 32, 4
     saved = hk.tk_kernel.get_narrow()
-    # T*k = 1200 > E*32: the late join runs with share 2
-    hk.tk_kernel.set_narrow(16, 32, share)
+    hk.tk_kernel.set_narrow(16, max_rows, share)
     try:
         gen = torch.Generator(device="cuda").manual_seed(77 + share)
         w13_q, w13_s = hk.quant_block(torch.randn((e, 2 * i, h), generator=gen, device="cuda"))
@@ -130,10 +133,10 @@ def test_moe_layer_graph_replay_narrow(hk, share):
             lg = lg - 1.1 * torch.log(rank)[None, :]
             sets.append((x_q, x_s, lg))
             r = hk.moe_forward_steps(x_q, x_s, lg, layer.w13_q, w13_s, layer.w2_q, w2_s, k, packed=True,
-                                     narrow=(16, 32, share))
+                                     narrow=(16, max_rows, share))
             torch.cuda.synchronize()
             counts = r["counts"].cpu()
-            assert int(r["narrow_info"][0]) > 0 and (counts > 32).any()
+            assert int(r["narrow_info"][0]) > 0 and (counts > max_rows).any()
         _replay_and_check(layer, sets)
     finally:
         hk.tk_kernel.set_narrow(*saved)

@@ -1,5 +1,7 @@
 """Narrow path of the one-call layer (experts of <= 64 rows in the
-weight-streaming kernel on an auxiliary stream) against the 256x256 kernels.
+weight-streaming kernel, on an auxiliary stream beside the 256x256 kernels, or
+after them on the caller's stream when T*k <= 2*E*max_rows) against the
+256x256 kernels.
 
 The narrow kernel uses the 256x256 kernel's operand order, block-scale arithmetic
 and epilogue, so the layer output is bit-identical with the narrow path off,
@@ -76,8 +78,10 @@ def test_narrow_bit_exact(hk, narrow_restore, name, packed):
     hk.tk_kernel.set_narrow(0, 64, 0)
     off = _one_call(hk, g, w13, w2, packed).clone()
     assert torch.equal(off.view(torch.int16), steps["out"].view(torch.int16))
-    # threshold 16 with wide_share 2: where T*k > 16*E (p8_g2_g1, p4_p2, dsv3_shape)
-    # the narrow CUs also join the first 256x256 GEMM's tiles (late join)
+    # threshold 64: every case here has T*k <= 2*E*64 (one stream); threshold 16:
+    # where T*k > 2*16*E (p8_g2_g1, dsv3_shape) the narrow kernels run on the
+    # auxiliary stream, and with wide_share 2 their CUs also join the first
+    # 256x256 GEMM's tiles (late join)
     print(f"  experts of 1..16 rows: {int(((counts > 0) & (counts <= 16)).sum())}", flush=True)
     # (4096, 64, 1): more CUs than the device has; the library keeps a quarter
     # of them for the first 256x256 GEMM
