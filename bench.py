@@ -19,10 +19,19 @@ configs 1 and 4 (per-tensor scales, bf16 out) and the reference MXFP8
 harness's 8192^3 shape with 1x32 e8m0 scales (fp32 out); ``value`` is then that
 GEMM's TFLOP/s.
 
-Extra JSON fields: ``roofline`` (dominant kernel: grouped GEMM 1, timed with
-events on the stream it runs on), ``cpu_baseline`` (the oracle's dequantise +
-fp32 per-expert matmul path on a bounded sample of experts, host cores),
-``kernels`` (per-kernel average ms from an event-timed stepwise pass).
+Timing: W warm-up calls, then ``settle`` (at least --settle-s seconds of
+back-to-back layer calls, recorded), then the K timed steps (wall clock,
+synchronised on both sides), then K more one-call layers with the library's
+per-dispatch timing events (hkmoe_kernel_timing) in the same steady state.
+
+Extra JSON fields: ``roofline`` (dominant kernel: the 256x256 grouped GEMM 1,
+its average duration from the per-dispatch events), ``kernels_ms`` (average
+duration of each kernel of the one-call layer) and ``kernel_timing`` (the
+layer's mean timeline, its span, the main-stream chain of kernels and the gaps
+between them), ``settle``, and ``cpu_baseline``: bench.py's own PyTorch CPU
+port of the layer (route, dequantise to fp32, per-expert x_e . W_e^T, SiLU*up,
+bf16, requantise, . W2_e^T, combine; kind "port", it does not use the oracle)
+timed on the host's cores over a bounded, size-stratified sample of experts.
 """
 import argparse
 import json
@@ -61,6 +70,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle-s", type=float, default=1.0,
+                    help="MoE workloads: seconds of back-to-back layer calls between the warm-up and the "
+                         "timed steps (recorded as `settle`)")
     ap.add_argument("--config", default="dsv3", choices=sorted(CONFIGS) + sorted(DENSE))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
@@ -341,6 +353,89 @@ def kernel_breakdown_narrow(inp, layer, narrow, iters=10):
     return ms, r
 
 
+def settle_run(step, seconds):
+    """Back-to-back layer calls for at least `seconds` (synchronised at the
+    end), run between the warm-up and the timed steps so that the timed steps
+    start in the clock and power state that sustained calls settle into."""
+    import torch
+    calls = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            step()
+        calls += 10
+        torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    return {"seconds": round(el, 3), "calls": calls, "ms_per_call": round(el / calls * 1e3, 4) if calls else None}
+
+
+# Layer roles on the main stream, in launch order (the critical path when the
+# narrow kernels run on the auxiliary stream beside the 256x256 GEMM 1).
+CHAIN = ("route_topk", "expert_block_scan", "expert_offsets", "scatter", "mx_gather_words", "grouped_gemm1",
+         "requant", "grouped_gemm2", "combine")
+
+
+def layer_kernel_timing(step, calls):
+    """Per-kernel times of `calls` one-call layers, measured by the library's
+    per-dispatch events (hkmoe_kernel_timing: each kernel's own start and end
+    timestamps, no marker packets between kernels).  Returns the mean duration
+    of each kernel role, the mean start/end of each role from the start of the
+    call's first kernel (timeline), the mean span of a call (first kernel start
+    to last kernel end) and the wall-clock ms per call of these timed calls."""
+    import torch
+    import tk_kernel
+    roles = tk_kernel.TIMING_ROLES
+    torch.cuda.synchronize()
+    tk_kernel.kernel_timing(calls)
+    try:
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            step()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / calls * 1e3
+        per = [tk_kernel.kernel_timing_read(i) for i in range(calls)]
+    finally:
+        tk_kernel.kernel_timing(0)
+    dur, beg, end = {}, {}, {}
+    for i, name in enumerate(roles):
+        got = [c[i] for c in per if c[i][0] >= 0]
+        if got:
+            dur[name] = sum(e - b for b, e in got) / len(got)
+            beg[name] = sum(b for b, _ in got) / len(got)
+            end[name] = sum(e for _, e in got) / len(got)
+    span = sum(max(e for _, e in c) for c in per) / calls
+    # with the one-stream schedule the narrow kernels follow the 256x256 ones on
+    # the caller's stream and belong to the chain
+    one_stream = "narrow_gemm1" in dur and beg["narrow_gemm1"] >= end.get("grouped_gemm1", 0.0)
+    chain = sum(dur[n] for n in CHAIN + (("narrow_gemm1", "narrow_gemm2") if one_stream else ()) if n in dur)
+    res = {"kernels_ms": dur, "calls": calls, "wall_ms_per_call": round(wall, 4), "span_ms": round(span, 4),
+           "chain_sum_ms": round(chain, 4), "chain_gaps_ms": round(span - chain, 4),
+           "timeline_ms": {n: [round(beg[n], 4), round(end[n], 4)] for n in dur}}
+    if "narrow_gemm1" in dur and "grouped_gemm1" in dur:
+        res["gemm1_span_ms"] = (max(end["grouped_gemm1"], end["narrow_gemm1"]) -
+                                min(beg["grouped_gemm1"], beg["narrow_gemm1"]))
+    return res
+
+
+def route_counts(inp):
+    """Rows per expert of the benched routing (the path's own routing kernels)."""
+    import torch
+    import tk_kernel
+    logits, k = inp["logits"], inp["top_k"]
+    T, E = logits.shape
+    dev = logits.device
+    nblk = tk_kernel.route_blocks(T)
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    bc = torch.empty((nblk, E), dtype=torch.int32, device=dev)
+    tk_kernel.dispatch_route_topk(logits, idx, w, bc)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offs = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    mto = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    tk_kernel.dispatch_expert_offsets(bc, T, counts, offs, torch.empty_like(bc), mto, None)
+    return counts.cpu()
+
+
 def cpu_threads():
     """Host threads of the CPU baseline: the machine's cores (os.cpu_count()),
     capped by OMP_NUM_THREADS when the environment sets it (the GPU boxes give
@@ -488,7 +583,8 @@ PROF_TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d {d}/t
 PROF_TRACE_CMD_DENSE = ("rocprofv3 --kernel-trace --stats --output-format csv -d {d}/trace -o run -- "
                         "python3 bench.py --config {c} --steps 40 --warmup 5 --no-cpu > {d}/bench.json")
 PROF_PMC_CMD = ("rocprofv3 --pmc {ctr} --output-format csv -d {d}/{ctr} -o run -- "
-                "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu --other-configs '' --calibrate-copy")
+                "python3 bench.py --config {c} --steps 2 --warmup 1 --settle-s 0 --no-cpu --other-configs '' "
+                "--calibrate-copy")
 CALIB_BYTES = 1 << 30
 
 
@@ -605,20 +701,21 @@ def summarize_profile(args):
         else:
             f.write(f"bench line of the traced run: value {b['value']} {b['unit']}, "
                     f"{b['ms_per_step']} ms/step, weights {b['config'].get('weights')}, "
-                    f"active experts {b['config']['active_experts']}, event-timed kernels (ms): "
+                    f"active experts {b['config']['active_experts']}, kernel averages from per-dispatch events (ms): "
                     f"{json.dumps(b['kernels_ms'])}\n\n")
         if dense:
             f.write("Command (repo root; the GEMM's call count includes the warmup calls):\n\n")
             f.write("    " + PROF_TRACE_CMD_DENSE.format(d="<out>", c=args.config) + "\n\n")
         else:
-            f.write("Command (repo root; bench.py runs warmup + timed steps + a 10-iteration "
-                    "per-kernel pass, so call counts include all of them):\n\n")
+            f.write("Command (repo root; bench.py runs warm-up calls, the settle calls, the timed steps and "
+                    "as many calls with per-dispatch timing events, so call counts include all of them):\n\n")
             f.write("    " + PROF_TRACE_CMD.format(d="<out>", c=args.config) + "\n\n")
         f.write("| kernel | calls | avg us | min us | max us | share of library time |\n|---|---|---|---|---|---|\n")
         for lab, n, avg, mn, mx, t in sorted(rows, key=lambda r: -r[5]):
             f.write(f"| {lab} | {n} | {avg:.1f} | {mn:.1f} | {mx:.1f} | {100 * t / tot:.1f}% |\n")
         if not dense:
-            _write_timeline(f, os.path.join(d, "trace", "run_kernel_trace.csv"), b["warmup"] + b["steps"])
+            _write_timeline(f, os.path.join(d, "trace", "run_kernel_trace.csv"),
+                            b["warmup"] + b.get("settle", {}).get("calls", 0) + b["steps"])
     # traffic passes
     per = {}
     calib = {}
@@ -700,7 +797,7 @@ PMC_PASSES = {
     "mem": "TCP_TCC_READ_REQ_LATENCY_sum TCP_TCC_READ_REQ_sum TCP_PENDING_STALL_CYCLES_sum GRBM_GUI_ACTIVE",
 }
 PROF_PMC_PASS_CMD = ("rocprofv3 --pmc {ctrs} --output-format csv -d {d}/{p} -o run -- "
-                     "python3 bench.py --config {c} --steps 2 --warmup 1 --no-cpu --other-configs ''")
+                     "python3 bench.py --config {c} --steps 2 --warmup 1 --settle-s 0 --no-cpu --other-configs ''")
 
 
 def summarize_counters(args):
@@ -958,6 +1055,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    settle = settle_run(step, args.settle_s)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
@@ -965,6 +1063,11 @@ def main():
     dt = (time.perf_counter() - t0) / args.steps
     flops = gemm_flops(cfg)
     value = flops / dt / 1e12
+    # the same steady state: the next `steps` one-call layers (eager) with
+    # per-dispatch timing events
+    eager = lambda: layer(inp["x_q"], inp["x_scale"], inp["logits"], out=out)
+    kt = layer_kernel_timing(eager, max(args.steps, 1))
+    ms = kt["kernels_ms"]
 
     if args.calibrate_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -972,10 +1075,9 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    ms, r = kernel_breakdown(inp, layer)
     rows = cfg["T"] * cfg["k"]
-    counts = r["counts"].cpu()
-    narrow = r.get("narrow_info") is not None
+    counts = route_counts(inp)
+    narrow = "narrow_gemm1" in ms
     narrow_rows = 0
     if narrow:
         _, max_rows, _ = narrow_setting(inp)
@@ -984,7 +1086,7 @@ def main():
         n_narrow = int(small.sum())
     # the dominant kernel is the 256x256 GEMM 1 over the rows it processes
     g1_flops = 2.0 * (rows - narrow_rows) * 2 * cfg["I"] * cfg["H"]
-    g1_tflops = g1_flops / (ms["grouped_gemm1"] * 1e-3) / 1e12
+    g1_tflops = g1_flops / (ms["grouped_gemm1"] * 1e-3) / 1e12 if "grouped_gemm1" in ms else 0.0
     traffic = None
     if os.path.exists(args.traffic):
         try:
@@ -1012,7 +1114,9 @@ def main():
                      "achieved": round(g1_tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(g1_tflops / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
                      "avg_ms": round(ms["grouped_gemm1"], 4), "flops_per_launch": g1_flops},
+        "settle": settle,
         "kernels_ms": {k: round(v, 4) for k, v in ms.items()},
+        "kernel_timing": {k: v for k, v in kt.items() if k != "kernels_ms"},
         "gemm_only_tflops": round(flops / ((ms["grouped_gemm1"] + ms["grouped_gemm2"]) * 1e-3) / 1e12, 2),
     }
     if narrow:
@@ -1026,8 +1130,8 @@ def main():
                       "GB_s": round(nb1 / ms["narrow_gemm1"] / 1e6, 1)},
             "gemm2": {"ms": round(ms["narrow_gemm2"], 4), "weight_bytes": nb2,
                       "GB_s": round(nb2 / ms["narrow_gemm2"] / 1e6, 1)},
-            "gemm1_span_ms": round(ms["gemm1_span"], 4),
-            "gemm1_span_tflops": round(2.0 * rows * 2 * cfg["I"] * cfg["H"] / (ms["gemm1_span"] * 1e-3) / 1e12, 2),
+            "gemm1_span_ms": round(kt["gemm1_span_ms"], 4),
+            "gemm1_span_tflops": round(2.0 * rows * 2 * cfg["I"] * cfg["H"] / (kt["gemm1_span_ms"] * 1e-3) / 1e12, 2),
         }
         if narrow_rows == rows:
             # every expert is narrow (decode-like): the dominant kernel is the

@@ -5,6 +5,7 @@
 // no allocation happens in any entry point: callers own every buffer, as with
 // the reference's dispatch functions (include/pyutils/pyutils.cuh:54-71,
 // kernels/cdna3/.../256_256_64_32.cpp:202-206).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -19,8 +20,10 @@
 #include "gemm_small.hpp"
 #include "moe_kernels.hpp"
 
+#include <atomic>
 #include <cstdlib>
 #include <mutex>
+#include <vector>
 
 using namespace hkmoe;
 
@@ -44,6 +47,70 @@ int check_launch(const char* what) {
   if (err != hipSuccess) return fail(HKMOE_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
   return HKMOE_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Kernel timing of the layer entry points (hkmoe_kernel_timing).  While it is
+// on, each kernel a layer call enqueues is launched by hipExtLaunchKernelGGL
+// with a pair of library-owned events that take that dispatch's own start and
+// end timestamps: no marker packet goes between the kernels, so the timed
+// calls keep the untimed schedule.  One set of events per call, in a ring of
+// `calls` sets; t_slot is the set of the call being enqueued (-1: untimed) and
+// t_role the kernel role about to be launched.
+// ---------------------------------------------------------------------------
+struct KernelTiming {
+  int calls = 0;                 // ring size, 0: off
+  int next = 0;                  // next call's set
+  int device = -1;
+  std::vector<hipEvent_t> ev;    // [calls][HKMOE_TIMING_ROLES][2]
+  std::vector<uint8_t> used;     // [calls][HKMOE_TIMING_ROLES]
+  std::vector<int> first, last;  // [calls]: roles of the call's first and last launch
+};
+KernelTiming g_timing;
+std::mutex g_timing_mu;
+thread_local int t_slot = -1;
+thread_local int t_role = -1;
+
+// The events of the launch about to be made (false: launch untimed).
+bool timing_events(hipEvent_t* start, hipEvent_t* stop) {
+  if (t_slot < 0 || t_role < 0 || t_role >= HKMOE_TIMING_ROLES) return false;
+  const size_t i = static_cast<size_t>(t_slot) * HKMOE_TIMING_ROLES + t_role;
+  *start = g_timing.ev[2 * i];
+  *stop = g_timing.ev[2 * i + 1];
+  g_timing.used[i] = 1;
+  if (g_timing.first[t_slot] < 0) g_timing.first[t_slot] = t_role;
+  g_timing.last[t_slot] = t_role;
+  return true;
+}
+
+// Every kernel of the layer entry points goes through here.
+template <typename... Kargs, typename... Args>
+void hk_launch(void (*kern)(Kargs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t stream, Args... args) {
+  hipEvent_t a, b;
+  if (timing_events(&a, &b))
+    hipExtLaunchKernelGGL(kern, grid, block, lds, stream, a, b, 0u, static_cast<Kargs>(args)...);
+  else
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, static_cast<Kargs>(args)...);
+}
+
+// Marks the launches of one layer call as timed (a set of the ring) for its
+// lifetime; does nothing while timing is off or on another device.
+struct TimedCall {
+  bool on = false;
+  TimedCall() {
+    std::lock_guard<std::mutex> g(g_timing_mu);
+    int dev = -1;
+    if (g_timing.calls <= 0 || hipGetDevice(&dev) != hipSuccess || dev != g_timing.device) return;
+    t_slot = g_timing.next;
+    g_timing.next = (g_timing.next + 1) % g_timing.calls;
+    std::fill_n(g_timing.used.begin() + static_cast<size_t>(t_slot) * HKMOE_TIMING_ROLES, HKMOE_TIMING_ROLES, 0);
+    g_timing.first[t_slot] = g_timing.last[t_slot] = -1;
+    on = true;
+  }
+  ~TimedCall() {
+    if (on) t_slot = -1;
+    t_role = -1;
+  }
+};
 
 #define HK_REQUIRE(cond, ...)                                 \
   do {                                                        \
@@ -89,18 +156,24 @@ int launch_gemm(GemmParams p, hipStream_t stream, int grid_override = 0) {
     attr_set[dev] = true;
   }
   const int grid = grid_override > 0 ? grid_override : device_cus();
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), kLdsBytes, stream, p);
+  hk_launch(kern, dim3(grid), dim3(kThreads), kLdsBytes, stream, p);
   return check_launch("gemm_fp8_persistent");
 }
 
+// MFMA shape of the 128x128-tile dense kernel (hkmoe_set_dense_mfma): 16 or 32.
+// 32x32x64 is the default: 2048^3 runs in 14.0 vs 15.1 us, 1024x4096x4096 in
+// 23.2 vs 24.7 us, 4096x2048x1024 in 16.8 vs 17.1 us (graph-replayed launches,
+// rotating operand copies, best of three interleaved rounds on one box).
+std::atomic<int> g_dense_mfma{32};
+
 // The dense GEMM on 128x128 tiles (gemm_small.hpp): one workgroup per tile,
 // the grid a whole number of 4x8 tile blocks.
-template <bool F32OUT>
+template <bool F32OUT, bool M32>
 int launch_gemm_small(const SmallGemmParams& p, hipStream_t stream) {
   static bool attr_set[kMaxDevices] = {false};
   int dev = 0;
   (void)hipGetDevice(&dev);
-  auto kern = gemm_fp8_small<F32OUT>;
+  auto kern = gemm_fp8_small<F32OUT, M32>;
   if (dev >= 0 && dev < kMaxDevices && !attr_set[dev]) {
     const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, kSmLdsBytes);
@@ -133,7 +206,7 @@ int launch_narrow_p(const GemmParams& p, hipStream_t stream, int grid) {
     if (err != hipSuccess) return fail(HKMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(err));
     attr_set[dev] = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, stream, p);
+  hk_launch(kern, dim3(grid), dim3(kThreads), lds, stream, p);
   return check_launch("gemm_fp8_narrow");
 }
 
@@ -268,11 +341,14 @@ int launch_expert_offsets(const int32_t* block_counts, int64_t num_tokens, int32
                           int32_t* tile_counters, int narrow_max, int32_t* narrow_info,
                           hipStream_t stream) {
   const int nblk = route_blocks(num_tokens);
-  hipLaunchKernelGGL(expert_block_scan_kernel, dim3((num_experts + kOffExperts - 1) / kOffExperts),
-                     dim3(kScanThreads), 0, stream, block_counts, nblk, num_experts, counts, block_base);
+  const bool timed = t_role == HKMOE_TIMING_OFFSETS;
+  if (timed) t_role = HKMOE_TIMING_BLOCK_SCAN;
+  hk_launch(expert_block_scan_kernel, dim3((num_experts + kOffExperts - 1) / kOffExperts),
+            dim3(kScanThreads), 0, stream, block_counts, nblk, num_experts, counts, block_base);
   HK_TRY(check_launch("expert_block_scan_kernel"));
-  hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(kScanThreads), 0, stream, num_experts, counts, offsets,
-                     mtile_offsets, mtile_list, kBM, amax_reset, tile_counters, narrow_max, narrow_info);
+  if (timed) t_role = HKMOE_TIMING_OFFSETS;
+  hk_launch(expert_offsets_kernel, dim3(1), dim3(kScanThreads), 0, stream, num_experts, counts, offsets,
+            mtile_offsets, mtile_list, kBM, amax_reset, tile_counters, narrow_max, narrow_info);
   return check_launch("expert_offsets_kernel");
 }
 
@@ -307,6 +383,14 @@ int hkmoe_get_narrow(int32_t* cus, int32_t* max_rows, int32_t* wide_share) {
 
 const char* hkmoe_last_error(void) { return g_last_error.c_str(); }
 
+int hkmoe_set_dense_mfma(int32_t shape) {
+  HK_REQUIRE(shape == 16 || shape == 32, "set_dense_mfma: shape=%d must be 16 or 32", shape);
+  g_dense_mfma.store(shape);
+  return HKMOE_OK;
+}
+
+int hkmoe_get_dense_mfma(void) { return g_dense_mfma.load(); }
+
 int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k,
                    const float* scale_a, const float* scale_b, int out_dtype, hkmoe_stream_t stream) {
   HK_REQUIRE(b && (m == 0 || (a && c)), "gemm_fp8: null tensor pointer");
@@ -314,8 +398,8 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
              (long long)n, (long long)k);
   HK_REQUIRE(k % 128 == 0, "gemm_fp8: K=%lld must be a multiple of 128", (long long)k);
   HK_REQUIRE(n % kBN == 0, "gemm_fp8: N=%lld must be a multiple of 256", (long long)n);
-  HK_REQUIRE(k <= (1 << 20) && n * k < (1ll << 32) && m < (1ll << 31),
-             "gemm_fp8: operand too large for 32-bit buffer offsets");
+  HK_REQUIRE(k <= (1 << 20) && n * k < (1ll << 32) && m * k < (1ll << 32) && m < (1ll << 31),
+             "gemm_fp8: operand too large for 32-bit buffer offsets (M*K and N*K must be < 2^32)");
   HK_REQUIRE(out_dtype == HKMOE_BF16 || out_dtype == HKMOE_F32, "gemm_fp8: bad out_dtype %d", out_dtype);
   if (m == 0) return HKMOE_OK;
   auto s = static_cast<hipStream_t>(stream);
@@ -335,7 +419,9 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
     q.m_tiles = static_cast<int32_t>((m + kSmTile - 1) / kSmTile);
     q.n_tiles = static_cast<int32_t>(n / kSmTile);
     q.nbn = (q.n_tiles + 7) / 8;
-    return out_dtype == HKMOE_BF16 ? launch_gemm_small<false>(q, s) : launch_gemm_small<true>(q, s);
+    if (g_dense_mfma.load() == 32)
+      return out_dtype == HKMOE_BF16 ? launch_gemm_small<false, true>(q, s) : launch_gemm_small<true, true>(q, s);
+    return out_dtype == HKMOE_BF16 ? launch_gemm_small<false, false>(q, s) : launch_gemm_small<true, false>(q, s);
   }
   GemmParams p{};
   p.a = static_cast<const uint8_t*>(a);
@@ -372,9 +458,8 @@ int hkmoe_route_topk(const float* logits, int64_t num_tokens, int32_t num_expert
             : per_lane <= 4 ? route_topk_kernel<4> : per_lane <= 8 ? route_topk_kernel<8>
             : per_lane <= 16 ? route_topk_kernel<16> : per_lane <= 32 ? route_topk_kernel<32>
                              : route_topk_kernel<64>;
-  hipLaunchKernelGGL(kern, dim3(route_blocks(num_tokens)), dim3(kTopkThreads), 0,
-                     static_cast<hipStream_t>(stream), logits, static_cast<int>(num_tokens),
-                     num_experts, top_k, topk_idx, topk_w, block_counts);
+  hk_launch(kern, dim3(route_blocks(num_tokens)), dim3(kTopkThreads), 0, static_cast<hipStream_t>(stream), logits,
+            static_cast<int>(num_tokens), num_experts, top_k, topk_idx, topk_w, block_counts);
   return check_launch("route_topk_kernel");
 }
 
@@ -431,7 +516,7 @@ int hkmoe_scatter(const int32_t* topk_idx, int64_t num_tokens, int32_t num_exper
     }
   }
   if (num_tokens == 0) return HKMOE_OK;
-  hipLaunchKernelGGL(scatter_kernel, dim3(route_blocks(num_tokens)), dim3(kRouteThreads), 0,
+  hk_launch(scatter_kernel, dim3(route_blocks(num_tokens)), dim3(kRouteThreads), 0,
                      static_cast<hipStream_t>(stream), topk_idx, static_cast<int>(num_tokens),
                      num_experts, top_k, offsets, block_base, perm, inv_perm,
                      static_cast<const uint8_t*>(x_q), x_scale, hidden,
@@ -542,7 +627,7 @@ int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, co
   if (scale_mode == HKMOE_SCALE_BLOCK) {
     if (rows == 0) return HKMOE_OK;
     HK_REQUIRE(rows < (1ll << 31), "requant: too many rows");
-    hipLaunchKernelGGL(requant_group_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
+    hk_launch(requant_group_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, s,
                        static_cast<const uint16_t*>(h), rows, inter, static_cast<uint8_t*>(hq), hs);
     return check_launch("requant_group_kernel");
   }
@@ -550,7 +635,7 @@ int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, co
   HK_REQUIRE(amax != nullptr, "requant: per-tensor mode needs amax");
   const int64_t n8 = rows * inter / 8;
   const int grid = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, (n8 + 255) / 256), 4 * 1024));
-  hipLaunchKernelGGL(requant_tensor_kernel, dim3(grid), dim3(256), 0, s,
+  hk_launch(requant_tensor_kernel, dim3(grid), dim3(256), 0, s,
                      static_cast<const uint16_t*>(h), n8, amax, static_cast<uint8_t*>(hq), hs);
   return check_launch("requant_tensor_kernel");
 }
@@ -704,7 +789,7 @@ int hkmoe_combine(const void* y, const float* topk_w, const int32_t* inv_perm, i
       threads = t;
       break;
     }
-  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(num_tokens)), dim3(threads), 0,
+  hk_launch(combine_kernel, dim3(static_cast<unsigned>(num_tokens)), dim3(threads), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(y), topk_w,
                      inv_perm, top_k, hidden, static_cast<uint16_t*>(out));
   return check_launch("combine_kernel");
@@ -786,7 +871,8 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
 }
 
 // The layer; aux_ok: the narrow path may fork to the library's auxiliary
-// stream (else every kernel runs on `stream`, with the narrow path off).
+// stream (else every kernel runs on `stream`: the one-stream narrow schedule
+// where it applies, otherwise the 256x256 kernels alone).
 static int moe_forward_impl(const void* x_q, const float* x_scale, const float* logits, const void* w13,
                             const float* w13_scale, const void* w2, const float* w2_scale,
                             int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
@@ -822,7 +908,7 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
   // the weight-streaming narrow kernels on an auxiliary stream, which run
   // beside the 256x256 kernels of the larger experts on the main stream.
   const NarrowConfig nc = narrow_config();
-  const bool narrow_ok = aux_ok && block && nc.cus > 0 && nc.max_rows > 0 && narrow_depth(hidden / kBK) > 0 &&
+  const bool narrow_ok = block && nc.cus > 0 && nc.max_rows > 0 && narrow_depth(hidden / kBK) > 0 &&
                          narrow_depth(inter / kBK) > 0;
   // Up to 2*max_rows rows per expert on average (T*k <= 2*E*max_rows) the small
   // experts' weight stream dominates: the narrow kernels then run on `stream`
@@ -832,35 +918,46 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
   // shape (H=7168, I=2048, E=256, k=8): T=512 / 1024 / 2048 / 4096 run 26 / 21 /
   // 13 / 4% faster on one stream, T=6144 / 8192 10 / 8% slower.
   const bool narrow_seq = narrow_ok && rows <= 2 * static_cast<int64_t>(num_experts) * nc.max_rows;
+  // the two-stream schedule needs the auxiliary stream; without it (aux_ok
+  // false) such layers run the 256x256 kernels alone
   AuxStreams* aux = nullptr;
-  if (narrow_ok && !narrow_seq) HK_TRY(get_aux(s, &aux));
+  if (aux_ok && narrow_ok && !narrow_seq) HK_TRY(get_aux(s, &aux));
   std::unique_lock<std::mutex> aux_lock(g_aux_mu, std::defer_lock);
   if (aux) aux_lock.lock();
+  TimedCall timed_call;
+  t_role = HKMOE_TIMING_ROUTE;
   HK_TRY(hkmoe_route_topk(logits, num_tokens, num_experts, top_k, w.topk_idx, w.topk_w,
                           w.block_counts, stream));
+  t_role = HKMOE_TIMING_OFFSETS;
   HK_TRY(launch_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets,
                                w.block_base, w.mtile_offsets, w.mtile_list, w.amax, w.tile_ctr,
                                (aux || narrow_seq) ? nc.max_rows : 0,
                                (aux || narrow_seq) ? w.narrow_info : nullptr, s));
+  t_role = HKMOE_TIMING_SCATTER;
   HK_TRY(hkmoe_scatter(w.topk_idx, num_tokens, num_experts, top_k, w.offsets, w.block_base, w.perm,
                        w.inv_perm, nullptr, nullptr, hidden, scale_mode, nullptr, nullptr, stream));
   if (narrow_seq) {
     // one stream: each 256x256 GEMM keeps every CU (yield_from 0) and skips the
     // narrow experts' tiles; each narrow GEMM then runs its items on every CU
     const int ngrid = device_cus();
+    t_role = HKMOE_TIMING_GEMM1;
     HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream, w.narrow_info, 0, 0));
+    t_role = HKMOE_TIMING_GEMM1_NARROW;
     HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.narrow_info + 1, stream, w.narrow_info, 0,
                               ngrid, ngrid));
+    t_role = HKMOE_TIMING_GEMM2;
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.tile_ctr + 8, stream,
                               w.narrow_info, 0, 0));
+    t_role = HKMOE_TIMING_GEMM2_NARROW;
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.narrow_info + 2, stream,
                               w.narrow_info, 0, ngrid, ngrid));
+    t_role = HKMOE_TIMING_COMBINE;
     HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
     return HKMOE_OK;
   }
@@ -881,10 +978,12 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
     // the narrow kernels launch one workgroup per CU: beside 256x256 tiles the
     // first ncus to start take items, else all of them (decode-like shapes)
     const int ngrid = device_cus();
+    t_role = HKMOE_TIMING_GEMM1_NARROW;
     HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.narrow_info + 1, aux->aux,
                               w.narrow_info, 0, ncus, ngrid));
+    t_role = HKMOE_TIMING_GEMM2_NARROW;
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.narrow_info + 2,
                               aux->aux, w.narrow_info, 0, ncus, ngrid));
@@ -893,6 +992,7 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
     // takes whatever tiles are left); the second 256x256 GEMM then waits for both.
     // (Shapes with rows <= 2 * E * max_rows took the one-stream path above.)
     const bool late_join = nc.share == 2;
+    t_role = HKMOE_TIMING_GEMM1_JOIN;
     if (late_join)
       HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                                 w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
@@ -900,12 +1000,14 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
                                 -1, 0, ncus));
     if (hipEventRecord(aux->join, aux->aux) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: join event failed");
+    t_role = HKMOE_TIMING_GEMM1;
     HK_TRY(grouped_gemm1_impl(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                               w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter, scale_mode,
                               w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream, w.narrow_info,
                               yield_from, 0));
     if (late_join && hipStreamWaitEvent(s, aux->join, 0) != hipSuccess)
       return fail(HKMOE_ERR_HIP, "moe_forward: join of the auxiliary stream failed");
+    t_role = HKMOE_TIMING_GEMM2;
     HK_TRY(grouped_gemm2_impl(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                               num_experts, hidden, inter, scale_mode, w_layout, w.y, w.tile_ctr + 8,
                               stream, w.narrow_info, 0, 0));
@@ -913,24 +1015,30 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
       return fail(HKMOE_ERR_HIP, "moe_forward: join of the auxiliary stream failed");
     guard.armed = false;  // joined above
     aux_lock.unlock();
+    t_role = HKMOE_TIMING_COMBINE;
     HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
     return HKMOE_OK;
   }
   if (block) {
     // GEMM 1 reads token rows through perm and writes the requantised e4m3
     // intermediate and its 1x128 group scales directly.
+    t_role = HKMOE_TIMING_GEMM1;
     HK_TRY(hkmoe_grouped_gemm1(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                                w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter,
                                scale_mode, w_layout, HKMOE_E4M3, w.hq, w.hs, w.tile_ctr, stream));
   } else {
+    t_role = HKMOE_TIMING_GEMM1;
     HK_TRY(hkmoe_grouped_gemm1(x_q, x_scale, w.perm, top_k, num_tokens, w13, w13_scale, w.offsets,
                                w.mtile_offsets, w.mtile_list, rows, num_experts, hidden, inter,
                                scale_mode, w_layout, HKMOE_BF16, w.h, w.amax, w.tile_ctr, stream));
+    t_role = HKMOE_TIMING_REQUANT;
     HK_TRY(hkmoe_requant(w.h, rows, inter, scale_mode, w.amax, w.hq, w.hs, stream));
   }
+  t_role = HKMOE_TIMING_GEMM2;
   HK_TRY(hkmoe_grouped_gemm2(w.hq, w.hs, w2, w2_scale, w.offsets, w.mtile_offsets, w.mtile_list,
                              rows, num_experts, hidden, inter, scale_mode, w_layout, w.y,
                              w.tile_ctr + 8, stream));
+  t_role = HKMOE_TIMING_COMBINE;
   HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
   return HKMOE_OK;
 }
@@ -1027,9 +1135,9 @@ int hkmoe_gemm_mx(const void* a, const void* a_scale, const void* b, const void*
   HK_REQUIRE(k % kBK == 0, "gemm_mx: K=%lld must be a multiple of 128", (long long)k);
   HK_REQUIRE(n % kBN == 0, "gemm_mx: N=%lld must be a multiple of 256", (long long)n);
   const int64_t m64 = (m + 63) / 64 * 64;
-  HK_REQUIRE(k <= (1 << 20) && n * k < (1ll << 32) && m < (1ll << 31) && m64 * (k / 32) < (1ll << 32) &&
-                 n * (k / 32) < (1ll << 32),
-             "gemm_mx: operand too large for 32-bit buffer offsets");
+  HK_REQUIRE(k <= (1 << 20) && n * k < (1ll << 32) && m * k < (1ll << 32) && m < (1ll << 31) &&
+                 m64 * (k / 32) < (1ll << 32) && n * (k / 32) < (1ll << 32),
+             "gemm_mx: operand too large for 32-bit buffer offsets (M*K and N*K must be < 2^32)");
   HK_REQUIRE(out_dtype == HKMOE_BF16 || out_dtype == HKMOE_F32, "gemm_mx: bad out_dtype %d", out_dtype);
   if (m == 0) return HKMOE_OK;
   GemmParams p{};
@@ -1087,7 +1195,7 @@ int hkmoe_mx_gather_scales(const void* s, int64_t x_rows, int32_t k, const int32
   if (rows == 0) return HKMOE_OK;
   const int64_t ws = mx_words_per_step(rows, num_experts);
   const int grid = static_cast<int>(std::min<int64_t>((ws * (k / kBK) + 255) / 256, 8192));
-  hipLaunchKernelGGL(mx_gather_words_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+  hk_launch(mx_gather_words_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint8_t*>(s), k, gather, gather ? gather_div : 1, offsets, mtile_offsets,
                      num_experts, ws, static_cast<uint32_t*>(words));
   return check_launch("mx_gather_words_kernel");
@@ -1213,20 +1321,77 @@ int hkmoe_moe_forward_mx(const void* x_q, const void* x_e8m0, const float* logit
   const MoeWorkspace w = carve(static_cast<uint8_t*>(workspace), num_tokens, num_experts, top_k, hidden,
                                inter, HKMOE_SCALE_MX);
   const int64_t rows = num_tokens * top_k;
+  TimedCall timed_call;
+  t_role = HKMOE_TIMING_ROUTE;
   HK_TRY(hkmoe_route_topk(logits, num_tokens, num_experts, top_k, w.topk_idx, w.topk_w, w.block_counts, stream));
+  t_role = HKMOE_TIMING_OFFSETS;
   HK_TRY(hkmoe_expert_offsets(w.block_counts, num_tokens, num_experts, w.counts, w.offsets, w.block_base,
                               w.mtile_offsets, w.mtile_list, w.amax, w.tile_ctr, stream));
+  t_role = HKMOE_TIMING_SCATTER;
   HK_TRY(hkmoe_scatter(w.topk_idx, num_tokens, num_experts, top_k, w.offsets, w.block_base, w.perm, w.inv_perm,
                        nullptr, nullptr, hidden, HKMOE_SCALE_TENSOR, nullptr, nullptr, stream));
   // token exponents -> tile-aligned words in expert order (x rows stay in place)
+  t_role = HKMOE_TIMING_MX_WORDS;
   HK_TRY(hkmoe_mx_gather_scales(x_e8m0, num_tokens, hidden, w.perm, top_k, w.offsets, w.mtile_offsets,
                                 num_experts, rows, w.xw, stream));
+  t_role = HKMOE_TIMING_GEMM1;
   HK_TRY(hkmoe_grouped_gemm1_mx(x_q, w.xw, w.perm, top_k, num_tokens, w13, w13_words, w.offsets, w.mtile_offsets,
                                 w.mtile_list, rows, num_experts, hidden, inter, w_layout, HKMOE_E4M3, w.hq, w.hs,
                                 w.tile_ctr, stream));
+  t_role = HKMOE_TIMING_GEMM2;
   HK_TRY(hkmoe_grouped_gemm2_mx(w.hq, w.hs, w2, w2_words, w.offsets, w.mtile_offsets, w.mtile_list, rows,
                                 num_experts, hidden, inter, w_layout, w.y, w.tile_ctr + 8, stream));
+  t_role = HKMOE_TIMING_COMBINE;
   HK_TRY(hkmoe_combine(w.y, w.topk_w, w.inv_perm, num_tokens, top_k, hidden, out, stream));
+  return HKMOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// kernel timing of the layer entry points
+// ---------------------------------------------------------------------------
+int hkmoe_kernel_timing(int32_t calls) {
+  HK_REQUIRE(calls >= 0 && calls <= 4096, "kernel_timing: calls=%d outside [0, 4096]", calls);
+  std::lock_guard<std::mutex> g(g_timing_mu);
+  for (hipEvent_t e : g_timing.ev) (void)hipEventDestroy(e);
+  g_timing = KernelTiming{};
+  if (calls == 0) return HKMOE_OK;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(HKMOE_ERR_HIP, "kernel_timing: no device");
+  const size_t n = static_cast<size_t>(calls) * HKMOE_TIMING_ROLES * 2;
+  g_timing.ev.reserve(n);
+  for (size_t i = 0; i < n; ++i) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) {
+      for (hipEvent_t x : g_timing.ev) (void)hipEventDestroy(x);
+      g_timing = KernelTiming{};
+      return fail(HKMOE_ERR_HIP, "kernel_timing: hipEventCreate failed");
+    }
+    g_timing.ev.push_back(e);
+  }
+  g_timing.used.assign(static_cast<size_t>(calls) * HKMOE_TIMING_ROLES, 0);
+  g_timing.first.assign(calls, -1);
+  g_timing.last.assign(calls, -1);
+  g_timing.device = dev;
+  g_timing.calls = calls;
+  return HKMOE_OK;
+}
+
+int hkmoe_kernel_timing_read(int32_t set, float* begin_ms, float* end_ms, int32_t n) {
+  HK_REQUIRE(begin_ms && end_ms && n >= HKMOE_TIMING_ROLES, "kernel_timing_read: need %d floats per array",
+             HKMOE_TIMING_ROLES);
+  std::lock_guard<std::mutex> g(g_timing_mu);
+  HK_REQUIRE(set >= 0 && set < g_timing.calls, "kernel_timing_read: set=%d outside [0, %d)", set,
+             g_timing.calls);
+  const size_t base = static_cast<size_t>(set) * HKMOE_TIMING_ROLES;
+  const int f = g_timing.first[set];
+  for (int r = 0; r < HKMOE_TIMING_ROLES; ++r) {
+    begin_ms[r] = end_ms[r] = -1.0f;
+    if (f < 0 || !g_timing.used[base + r]) continue;
+    const hipEvent_t t0 = g_timing.ev[2 * (base + f)];
+    if (hipEventElapsedTime(&begin_ms[r], t0, g_timing.ev[2 * (base + r)]) != hipSuccess ||
+        hipEventElapsedTime(&end_ms[r], t0, g_timing.ev[2 * (base + r) + 1]) != hipSuccess)
+      return fail(HKMOE_ERR_HIP, "kernel_timing_read: events of set %d not complete", set);
+  }
   return HKMOE_OK;
 }
 

@@ -62,6 +62,13 @@ __device__ __forceinline__ void load_lds_4B(i32x4 rsrc, void* lds_base, int voff
 
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Buffer offset row * stride + add in unsigned 32-bit arithmetic (the buffer
+// instruction reads its offset as unsigned): operands up to 4 GiB, which the
+// host checks, address correctly and without signed overflow.
+__device__ __forceinline__ int buf_off(int row, int stride, int add) {
+  return static_cast<int>(static_cast<uint32_t>(row) * static_cast<uint32_t>(stride) + static_cast<uint32_t>(add));
+}
+
 // ---------------------------------------------------------------------------
 // MFMA: D(16x16 fp32) += A(16x128 e4m3) . B(16x128 e4m3)^T
 // Lane l supplies row (l % 16) of each operand and 32 bytes of its K range;
@@ -72,6 +79,16 @@ __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ f32x4 mfma_e4m3_16x16x128(const i32x8& a, const i32x8& b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// MFMA: D(32x32 fp32) += A(32x64 e4m3) . B(32x64 e4m3)^T (v_mfma_f32_32x32x64_f8f6f4,
+// twice the work of the 16x16x128 form in twice its cycles).  Lane l supplies
+// row (l % 32) of each operand and 32 of its 64 K bytes (the same assignment
+// for both operands); output: lane l holds D[8*(r/4) + 4*(l/32) + r%4][l % 32]
+// in register r = 0..15.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16 mfma_e4m3_32x32x64(const i32x8& a, const i32x8& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------

@@ -254,7 +254,7 @@ __device__ __forceinline__ void b_source(const GemmParams& p, int e, int nt, boo
     srd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K, static_cast<uint32_t>(p.nb) * p.K);
     const int ld_row = 8 * wg + (lane >> 3), ld_chunk = (lane & 7) ^ swz(ld_row);
     const int b_row0 = silu ? nt * 128 + ld_row : nt * kBN + ld_row;
-    voff = b_row0 * p.K + ld_chunk * 16;
+    voff = buf_off(b_row0, p.K, ld_chunk * 16);
     kstride = kBK;
   }
 }
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     const int ln = lane_here();
     const int lrow = 8 * wg + (ln >> 3), lchunk = (ln & 7) ^ swz(lrow);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a_voff[i] = a_row(c, wave_row0 + 32 * i + lrow, staged) * p.K + lchunk * 16;
+    for (int i = 0; i < 4; ++i) a_voff[i] = buf_off(a_row(c, wave_row0 + 32 * i + lrow, staged), p.K, lchunk * 16);
     if (scale_loader)
       as_voff = static_cast<int>(a_row(c, scale_slot_row(wave_row0 + wg * 64 + ln), staged) * p.as_rs) * 4;
     if constexpr (kMX) {
@@ -540,7 +540,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     for (int q = 0; q < 4; ++q) {
       const int i = grp * 4 + q;
       const int boff = kSilu ? (32 * (i >> 1) + ((i & 1) ? p.n_out : 0)) : 32 * i;
-      const int ioff = p.b_packed ? 32 * i * kBK : boff * p.K;
+      const int ioff = p.b_packed ? 32 * i * kBK : buf_off(boff, p.K, 0);
       load_lds_16B(b_srd, sb + (32 * i + 8 * wg) * kBK, b_voff, kt * b_kstride + ioff);
     }
   };

@@ -220,8 +220,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
       wvoff[2 * j] = (2 * f) * 1024 + lane * 16;
       wvoff[2 * j + 1] = (2 * f + 1) * 1024 + lane * 16;
     } else {
-      wvoff[2 * j] = frag_w[j] * p.K + (2 * lg) * 16;
-      wvoff[2 * j + 1] = frag_w[j] * p.K + (2 * lg + 1) * 16;
+      wvoff[2 * j] = buf_off(frag_w[j], p.K, (2 * lg) * 16);
+      wvoff[2 * j + 1] = buf_off(frag_w[j], p.K, (2 * lg + 1) * 16);
     }
   }
   // lane-constant LDS offsets within a ring stage: A fragment chunks of row
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
       ta = lds_read_i32(gidx_wave + 4 * ra) / p.gather_div;
       ts = lds_read_i32(gidx_wave + 4 * rs) / p.gather_div;
     }
-    L.a_voff = ta * p.K + ld_chunk * 16;
+    L.a_voff = buf_off(ta, p.K, ld_chunk * 16);
     L.as_voff = static_cast<int>(ts * p.as_rs) * 4;
   };
 

@@ -2,7 +2,9 @@
 // C[M,N] = (sa*sb) * A[M,K] . B[N,K]^T with per-tensor scales, bf16 or fp32 C.
 //
 // 128x128 output tiles, one non-persistent workgroup of 4 waves per tile, one
-// wave per SIMD, each wave 64x64 outputs (4x4 v_mfma_f32_16x16x128_f8f6f4).
+// wave per SIMD, each wave 64x64 outputs: 4x4 v_mfma_f32_16x16x128_f8f6f4 per
+// K step, or (M32) 2x2 blocks of 32x32 outputs, each two
+// v_mfma_f32_32x32x64_f8f6f4 (the two 64-byte halves of the K step).
 // With one wave per SIMD there is no ping-pong partner: the wave overlaps its
 // own LDS fragment reads of step kt+1 with its MFMAs of step kt (two register
 // sets of fragments), and a 4-deep LDS ring fed by buffer->LDS DMA keeps three
@@ -46,7 +48,7 @@ __device__ __forceinline__ void small_wait_stage(int n_newer) {
 }
 static_assert(kSmAhead <= 4, "small_wait_stage covers at most 3 newer stages");
 
-template <bool F32OUT>
+template <bool F32OUT, bool M32>
 __global__ __launch_bounds__(kSmThreads, 1) void gemm_fp8_small(SmallGemmParams p) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const int tid = threadIdx.x;
@@ -80,8 +82,8 @@ __global__ __launch_bounds__(kSmThreads, 1) void gemm_fp8_small(SmallGemmParams 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int ra = min(m0 + 32 * i + ld_row, p.m - 1);
-    a_voff[i] = ra * p.k + ld_chunk * 16;
-    b_voff[i] = (n0 + 32 * i + ld_row) * p.k + ld_chunk * 16;
+    a_voff[i] = buf_off(ra, p.k, ld_chunk * 16);
+    b_voff[i] = buf_off(n0 + 32 * i + ld_row, p.k, ld_chunk * 16);
   }
   auto issue = [&](int kt) __attribute__((always_inline)) {
     uint8_t* st = smem + (kt % kSmStages) * kSmStageBytes;
@@ -91,26 +93,62 @@ __global__ __launch_bounds__(kSmThreads, 1) void gemm_fp8_small(SmallGemmParams 
     for (int i = 0; i < 4; ++i)
       load_lds_16B(b_srd, st + kSmOperandBytes + (32 * i + 8 * wave) * kBK, b_voff[i], kt * kBK);
   };
-  // The wave's fragments of step kt: A sub-tiles (rows 64wm + 16i + l16) and B
-  // fragments (columns 64wn + 16j + l16).
+  // The wave's fragments of step kt.  16x16x128: A sub-tiles (rows 64wm + 16i
+  // + l16) and B fragments (columns 64wn + 16j + l16), K bytes 32lg .. +31.
+  // M32: fragment 2b + h is 32-row block b (rows 64wm + 32b + l32 of A, 64wn +
+  // 32b + l32 of B) and K half h: bytes 64h + 32g .. +31 (g = lane / 32), i.e.
+  // the 32-byte chunk pair 2h + g of the row; the rows of a block start at a
+  // multiple of 32, so the swizzle of row l32 is the lane constant f32.
+  const int l32 = lane & 31, g32 = lane >> 5;
+  const int f32 = swz(l32);
   auto read = [&](int kt, i32x8 (&af)[4], i32x8 (&bf)[4]) __attribute__((always_inline)) {
     const uint8_t* st = smem + (kt % kSmStages) * kSmStageBytes;
+    if constexpr (M32) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = read_frag(st, 64 * wm + 16 * i + l16, lg, fx);
+      for (int f = 0; f < 4; ++f) {
+        af[f] = read_frag(st, 64 * wm + 32 * (f >> 1) + l32, 2 * (f & 1) + g32, f32);
+        bf[f] = read_frag(st + kSmOperandBytes, 64 * wn + 32 * (f >> 1) + l32, 2 * (f & 1) + g32, f32);
+      }
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = read_frag(st + kSmOperandBytes, 64 * wn + 16 * j + l16, lg, fx);
+      for (int i = 0; i < 4; ++i) af[i] = read_frag(st, 64 * wm + 16 * i + l16, lg, fx);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[j] = read_frag(st + kSmOperandBytes, 64 * wn + 16 * j + l16, lg, fx);
+    }
   };
 
+  // accumulators: 16x16x128: acc[i][j] (4 values); M32: acc32[bi][bj] (16 values)
   f32x4 acc[4][4];
+  f32x16 acc32[2][2];
+  if constexpr (M32) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto mma = [&](const i32x8 (&af)[4], const i32x8 (&bf)[4]) __attribute__((always_inline)) {
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc32[i][j][r] = 0.f;
+  } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma_e4m3_16x16x128(bf[j], af[i], acc[i][j]);
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  auto mma = [&](const i32x8 (&af)[4], const i32x8 (&bf)[4]) __attribute__((always_inline)) {
+    if constexpr (M32) {
+      // both K halves of the four blocks; a block's second MFMA is issued three
+      // MFMAs after its first
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc32[i][j] = mfma_e4m3_32x32x64(bf[2 * j + h], af[2 * i + h], acc32[i][j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_e4m3_16x16x128(bf[j], af[i], acc[i][j]);
+    }
   };
 
   // Prologue: steps 0 .. kSmAhead-1 in flight, step 0's fragments in registers.
@@ -162,8 +200,52 @@ __global__ __launch_bounds__(kSmThreads, 1) void gemm_fp8_small(SmallGemmParams 
   if (kt < k_steps) step(kt, af0, bf0, af1, bf1);
 
   // ---- epilogue: lane holds row 64wm + 16i + l16, columns 64wn + 16j + 4lg .. +3
+  // (M32: row 64wm + 32bi + l32, columns 64wn + 32bj + 8q + 4g32 .. +3 in
+  // registers 4q .. 4q+3 of acc32[bi][bj])
   const float tens = (p.a_scale ? p.a_scale[0] : 1.0f) * (p.b_scale ? p.b_scale[0] : 1.0f);
-  if constexpr (F32OUT) {
+  if constexpr (M32 && F32OUT) {
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const int r = m0 + 64 * wm + 32 * bi + l32;
+      if (r < p.m) {
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+          float* dst = static_cast<float*>(p.c) + static_cast<int64_t>(r) * p.n + n0 + 64 * wn + 32 * bj + 4 * g32;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<float4*>(dst + 8 * q) =
+                float4{acc32[bi][bj][4 * q] * tens, acc32[bi][bj][4 * q + 1] * tens,
+                       acc32[bi][bj][4 * q + 2] * tens, acc32[bi][bj][4 * q + 3] * tens};
+        }
+      }
+    }
+  } else if constexpr (M32) {
+    // staged as below: row r, 16-byte chunk c = 8wn + 4bj + q, 8-byte half g32
+    __syncthreads();  // every wave is done with the ring
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+      const int r = 64 * wm + 32 * bi + l32;
+#pragma unroll
+      for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = 8 * wn + 4 * bj + q;
+          uint2 v;
+          v.x = pack_bf16x2(acc32[bi][bj][4 * q] * tens, acc32[bi][bj][4 * q + 1] * tens);
+          v.y = pack_bf16x2(acc32[bi][bj][4 * q + 2] * tens, acc32[bi][bj][4 * q + 3] * tens);
+          *reinterpret_cast<uint2*>(smem + r * 256 + ((c ^ (r & 15)) << 4) + g32 * 8) = v;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = tid + kSmThreads * u, r = idx >> 4, c = idx & 15;
+      if (m0 + r < p.m) {
+        const uint4 v = *reinterpret_cast<const uint4*>(smem + r * 256 + ((c ^ (r & 15)) << 4));
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + static_cast<int64_t>(m0 + r) * p.n + n0 + c * 8) = v;
+      }
+    }
+  } else if constexpr (F32OUT) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = m0 + 64 * wm + 16 * i + l16;

@@ -716,6 +716,23 @@ PYBIND11_MODULE(tk_kernel, m) {
     check(hkmoe_get_narrow(&c, &r, &w));
     return py::make_tuple(c, r, w);
   });
+  m.def("kernel_timing", [](int calls) { check(hkmoe_kernel_timing(calls)); },
+        "time the kernels of the next layer calls (per-dispatch events, a ring of `calls` sets); 0 = off",
+        py::arg("calls"));
+  m.def("kernel_timing_read", [](int set) {
+    std::vector<float> b(HKMOE_TIMING_ROLES), e(HKMOE_TIMING_ROLES);
+    check(hkmoe_kernel_timing_read(set, b.data(), e.data(), HKMOE_TIMING_ROLES));
+    py::list out;
+    for (int r = 0; r < HKMOE_TIMING_ROLES; ++r) out.append(py::make_tuple(b[r], e[r]));
+    return out;
+  }, "(start, end) ms of each role's kernel from the start of the call's first kernel ((-1, -1): not launched)",
+        py::arg("set"));
+  m.attr("TIMING_ROLES") = py::make_tuple("route_topk", "expert_block_scan", "expert_offsets", "scatter",
+                                          "mx_gather_words", "grouped_gemm1", "narrow_gemm1", "grouped_gemm1_join",
+                                          "requant", "grouped_gemm2", "narrow_gemm2", "combine");
+  m.def("set_dense_mfma", [](int shape) { check(hkmoe_set_dense_mfma(shape)); },
+        "MFMA shape (16 or 32) of the 128x128-tile dense GEMM kernel", py::arg("shape"));
+  m.def("get_dense_mfma", []() { return hkmoe_get_dense_mfma(); });
   m.def("route_blocks", [](int64_t t) { return hkmoe_route_blocks(t); });
   m.def("mtile_list_ints", &mtile_list_ints, "ints of an M-tile list for `rows` expert rows over E experts");
   m.def("version", []() { return hkmoe_version(); });

@@ -71,6 +71,19 @@ int hkmoe_gemm_fp8(const void* a, const void* b, void* c, int64_t m, int64_t n, 
                    hkmoe_stream_t stream);
 
 /*
+ * MFMA shape of hkmoe_gemm_fp8's kernel for small problems (fewer 256x256 tiles
+ * than two per CU, e.g. 2048^3), which runs 128x128 tiles: 16 for
+ * v_mfma_f32_16x16x128_f8f6f4, 32 for v_mfma_f32_32x32x64_f8f6f4 (the default:
+ * 4-7% faster at 2048^3 and similar shapes).
+ * Both give the same sums (fp32 accumulation in another order).  Replaces the
+ * choice between the reference's mfma1616128 and mfma323264 wrappers
+ * (include/cdna4/ops/warp/register/tile/mma.cuh:97-125).  Other values are
+ * rejected; the setting is process-wide.
+ */
+int hkmoe_set_dense_mfma(int32_t shape);
+int hkmoe_get_dense_mfma(void);
+
+/*
  * Routing step 1: top-k + softmax weights + per-block expert histogram.
  *   logits [T,E] fp32 -> topk_idx [T,k] int32, topk_w [T,k] fp32.
  *   Order: descending logit, ties to the lower expert id.  Weights: softmax
@@ -291,6 +304,38 @@ size_t hkmoe_moe_workspace_size(int64_t num_tokens, int32_t num_experts, int32_t
  */
 int hkmoe_set_narrow(int32_t cus, int32_t max_rows, int32_t wide_share);
 int hkmoe_get_narrow(int32_t* cus, int32_t* max_rows, int32_t* wide_share);
+
+/*
+ * Kernel timing of the layer entry points (measurement).  The reference times a
+ * kernel with a hipEvent pair around its launch (kernels/cdna4/gemm/mxfp8/
+ * MXFP8_4wave/4_wave.cu:517-571); here the events belong to the dispatches
+ * themselves, so a layer call is timed per kernel without marker packets
+ * between its kernels.
+ *   hkmoe_kernel_timing(calls): calls > 0 times the kernels of the following
+ *     hkmoe_moe_forward / hkmoe_moe_forward_mx / hkmoe_moe_forward_noalloc calls on
+ *     the current device, cycling over `calls` sets of events (call i uses set
+ *     i % calls, counting from this call); 0 turns it off.  Creates (and
+ *     frees) events: not for use under graph capture.
+ *   hkmoe_kernel_timing_read(set, begin_ms, end_ms, n): after the timed calls
+ *     completed (the caller synchronises), the start and end of each role's
+ *     kernel in ms from the start of the call's first kernel, or -1 for both
+ *     when the call launched no kernel of that role; n >= HKMOE_TIMING_ROLES.
+ */
+#define HKMOE_TIMING_ROUTE 0          /* route_topk */
+#define HKMOE_TIMING_BLOCK_SCAN 1     /* per-expert prefix over routing blocks */
+#define HKMOE_TIMING_OFFSETS 2        /* expert offsets, M-tile list, counters */
+#define HKMOE_TIMING_SCATTER 3        /* perm / inv_perm */
+#define HKMOE_TIMING_MX_WORDS 4       /* MX layer: activation exponent words */
+#define HKMOE_TIMING_GEMM1 5          /* grouped GEMM 1, 256x256 tiles */
+#define HKMOE_TIMING_GEMM1_NARROW 6   /* grouped GEMM 1, narrow experts */
+#define HKMOE_TIMING_GEMM1_JOIN 7     /* late-join launch of GEMM 1 (wide_share 2) */
+#define HKMOE_TIMING_REQUANT 8        /* per-tensor requantisation of h */
+#define HKMOE_TIMING_GEMM2 9          /* grouped GEMM 2, 256x256 tiles */
+#define HKMOE_TIMING_GEMM2_NARROW 10  /* grouped GEMM 2, narrow experts */
+#define HKMOE_TIMING_COMBINE 11       /* top-k weighted combine */
+#define HKMOE_TIMING_ROLES 12
+int hkmoe_kernel_timing(int32_t calls);
+int hkmoe_kernel_timing_read(int32_t set, float* begin_ms, float* end_ms, int32_t n);
 int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits, const void* w13,
                       const float* w13_scale, const void* w2, const float* w2_scale,
                       int64_t num_tokens, int32_t num_experts, int32_t top_k, int32_t hidden,
@@ -310,8 +355,11 @@ int hkmoe_moe_forward(const void* x_q, const float* x_scale, const float* logits
  * before any launch.  Largest T that fits: 509 for config-3 shapes (H=7168,
  * I=2048, E=256, top-8, block scales), 856 for config-5 shapes (H=4096, I=1536,
  * E=128, top-8), 655 for config-2 shapes (H=4096, I=14336, E=8, top-2,
- * per-tensor scales).  Every kernel runs on `stream` (the narrow path's auxiliary stream is
- * not used).  The first call on a device looks up that device's scratch
+ * per-tensor scales).  Every kernel runs on `stream`: the narrow path's auxiliary
+ * stream is not used, so block-scaled layers with T*k <= 2*E*max_rows (see
+ * hkmoe_set_narrow; every layer of the three shapes above that fits the scratch)
+ * take the one-stream narrow schedule, as hkmoe_moe_forward does, and larger
+ * ones run the 256x256 kernels alone.  The first call on a device looks up that device's scratch
  * address (hipGetSymbolAddress): make it outside graph capture.  All calls on
  * one device share its scratch and each call leaves its intermediates there:
  * calls that overlap in time on one device (other streams, other threads)

@@ -54,6 +54,30 @@ def test_gemm_argument_errors_are_host_side(lib):
     assert "multiple of 256" in _err(lib)
     assert lib.hkmoe_gemm_fp8(fake, fake, fake, i64(64), i64(256), i64(128), None, None, 7, None) == 1
     assert "out_dtype" in _err(lib)
+    # A of 4 GiB or more cannot be addressed by 32-bit buffer offsets: refused
+    # (M = 8192, N = 256, K = 2^20 would take the 128x128 path with M*K = 2^33)
+    assert lib.hkmoe_gemm_fp8(fake, fake, fake, i64(8192), i64(256), i64(1 << 20), None, None, 0, None) == 1
+    assert "M*K" in _err(lib)
+    assert lib.hkmoe_gemm_fp8(fake, fake, fake, i64(1 << 22), i64(256), i64(1024), None, None, 0, None) == 1
+    assert "M*K" in _err(lib)
+
+
+def test_dense_mfma_setting(lib):
+    saved = lib.hkmoe_get_dense_mfma()
+    assert saved in (16, 32)
+    assert lib.hkmoe_set_dense_mfma(ctypes.c_int32(8)) == 1
+    assert "16 or 32" in _err(lib)
+    assert lib.hkmoe_set_dense_mfma(ctypes.c_int32(32)) == 0 and lib.hkmoe_get_dense_mfma() == 32
+    assert lib.hkmoe_set_dense_mfma(ctypes.c_int32(saved)) == 0
+
+
+def test_kernel_timing_argument_errors(lib):
+    f = (ctypes.c_float * 16)()
+    assert lib.hkmoe_kernel_timing(ctypes.c_int32(-1)) == 1
+    assert lib.hkmoe_kernel_timing(ctypes.c_int32(0)) == 0  # off: no device work
+    assert lib.hkmoe_kernel_timing_read(ctypes.c_int32(0), f, f, ctypes.c_int32(16)) == 1
+    assert "outside" in _err(lib)
+    assert lib.hkmoe_kernel_timing_read(ctypes.c_int32(0), f, f, ctypes.c_int32(3)) == 1
 
 
 def test_routing_argument_errors(lib):
@@ -189,6 +213,8 @@ def test_mx_argument_errors(lib):
     assert "null" in _err(lib)
     assert lib.hkmoe_gemm_mx(fake, fake, fake, fake, fake, i64(64), i64(256), i64(128), 5, None) == 1
     assert "out_dtype" in _err(lib)
+    assert lib.hkmoe_gemm_mx(fake, fake, fake, fake, fake, i64(1 << 22), i64(256), i64(1024), 1, None) == 1
+    assert "M*K" in _err(lib)
     assert lib.hkmoe_gemm_mx(fake, fake, fake, fake, fake, i64(0), i64(256), i64(128), 1, None) == 0
 
 

@@ -21,9 +21,22 @@ def _pm1(rng, shape):
     return np.where(rng.integers(0, 2, shape) == 1, 0x38, 0xB8).astype(np.uint8)  # +1 / -1
 
 
+@pytest.fixture
+def dense_mfma(hk, request):
+    """MFMA shape of the 128x128-tile dense kernel for one test (16x16x128 or
+    32x32x64), restored afterwards."""
+    saved = hk.tk_kernel.get_dense_mfma()
+    hk.tk_kernel.set_dense_mfma(request.param)
+    yield request.param
+    hk.tk_kernel.set_dense_mfma(saved)
+
+
+# all four shapes have fewer 256x256 tiles than two per CU: the 128x128 kernel
+@pytest.mark.parametrize("dense_mfma", [16, 32], indirect=True)
 @pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 512, 1024), (2048, 2048, 2048), (77, 256, 384)])
-def test_pm1_known_answer_fp32(hk, m, n, k):
-    """+-1 operands: every output is an exact integer; fp32 output must match bit for bit."""
+def test_pm1_known_answer_fp32(hk, dense_mfma, m, n, k):
+    """+-1 operands: every output is an exact integer; fp32 output must match bit
+    for bit, with either MFMA shape of the small-problem kernel."""
     rng = np.random.default_rng(m + n + k)
     a = _pm1(rng, (m, k))
     b = _pm1(rng, (n, k))
@@ -32,6 +45,22 @@ def test_pm1_known_answer_fp32(hk, m, n, k):
     hk.tk_kernel.dispatch_micro(to_f8(a), to_f8(b), c)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(c.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("dense_mfma", [32], indirect=True)
+@pytest.mark.parametrize("m,n,k", [(1, 256, 128), (300, 768, 640), (2048, 2048, 2048)])
+def test_gemm_mfma32_bf16(hk, dense_mfma, m, n, k):
+    """The 32x32x64 kernel with scales and bf16 output against the oracle, and
+    against the 16x16x128 kernel's bf16 output (same fp32 sums up to order)."""
+    d = synth.make_dense(m, n, k, seed=m + 1)
+    ref = spec.gemm_fp8(d["a_q"], d["b_q"], d["sa"], d["sb"], out="f32")
+    args = (to_f8(d["a_q"]), to_f8(d["b_q"]), to_f32([d["sa"]]), to_f32([d["sb"]]))
+    c32 = hk.gemm_fp8(*args)
+    hk.tk_kernel.set_dense_mfma(16)
+    c16 = hk.gemm_fp8(*args)
+    torch.cuda.synchronize()
+    assert rel_err(bf16_np(c32), ref) <= TOL
+    assert rel_err(bf16_np(c32), bf16_np(c16)) <= 8e-3
 
 
 def test_dispatch_micro_4d_views(hk):

@@ -360,6 +360,49 @@ def test_routing_full_size(hk, name):
     assert _np(offs)[-1] == t * k
 
 
+def test_routing_many_blocks(hk):
+    """More than 2048 routing blocks (T > 65536): each block-scan thread then
+    covers more block counts than it keeps in registers and reads them twice.
+    Block counts, block bases, counts, offsets and the permutation: bit-exact
+    against the oracle (block_base = exclusive prefix of an expert's counts
+    over the 32-token routing blocks)."""
+    t, e, k = 70000, 8, 2
+    rng = np.random.default_rng(11)
+    logits = rng.standard_normal((t, e)).astype(np.float32)
+    idx_ref, w_ref = spec.route_topk(logits, k)
+    nblk = hk.tk_kernel.route_blocks(t)
+    assert nblk == (t + 31) // 32 and nblk > 64 * 32
+    print(f"routing T={t} E={e} k={k}: {nblk} blocks", flush=True)
+    idx = torch.empty((t, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((t, k), dtype=torch.float32, device="cuda")
+    bc = torch.empty((nblk, e), dtype=torch.int32, device="cuda")
+    hk.tk_kernel.dispatch_route_topk(to_f32(logits), idx, w, bc)
+    counts = torch.empty(e, dtype=torch.int32, device="cuda")
+    offs = torch.empty(e + 1, dtype=torch.int32, device="cuda")
+    bb = torch.full_like(bc, -1)
+    mto = torch.empty(e + 1, dtype=torch.int32, device="cuda")
+    hk.tk_kernel.dispatch_expert_offsets(bc, t, counts, offs, bb, mto, None)
+    perm = torch.empty(t * k, dtype=torch.int32, device="cuda")
+    inv = torch.empty(t * k, dtype=torch.int32, device="cuda")
+    hk.tk_kernel.dispatch_scatter(idx, offs, bb, perm, inv, None, None, None, None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_np(idx), idx_ref)
+    assert rel_err(_np(w), w_ref) <= 1e-6
+    blk = np.repeat(np.arange(nblk), 32)[:t]
+    bc_ref = np.zeros((nblk, e), np.int64)
+    for j in range(k):
+        np.add.at(bc_ref, (blk, idx_ref[:, j]), 1)
+    np.testing.assert_array_equal(_np(bc), bc_ref)
+    bb_ref = np.cumsum(bc_ref, axis=0) - bc_ref
+    np.testing.assert_array_equal(_np(bb), bb_ref)
+    c_ref, o_ref = spec.expert_counts_offsets(idx_ref, e)
+    np.testing.assert_array_equal(_np(counts), c_ref)
+    np.testing.assert_array_equal(_np(offs), o_ref)
+    p_ref, i_ref = spec.permutation(idx_ref, e)
+    np.testing.assert_array_equal(_np(perm), p_ref)
+    np.testing.assert_array_equal(_np(inv), i_ref)
+
+
 def test_quantisers_bit_exact(hk):
     rng = np.random.default_rng(9)
     x = (rng.standard_normal((256, 384)) * 3).astype(np.float32)

@@ -3,8 +3,10 @@
 
 Bar: bit-identical outputs (the same kernels; only the workspace differs), on
 two calls in a row on the same device, the second with fewer tokens, in both
-scale modes; a layer whose workspace exceeds the library's scratch is refused
-on the host with HKMOE_ERR_WORKSPACE.
+scale modes; with block scales these layers take the one-stream narrow
+schedule, which must also match the layer with the narrow path switched off;
+a layer whose workspace exceeds the library's scratch is refused on the host
+with HKMOE_ERR_WORKSPACE.
 """
 import ctypes
 import os
@@ -86,6 +88,16 @@ def test_noalloc_matches_workspace_entry_point(hk, lib, block):
         torch.cuda.synchronize()
         print(f"noalloc block={block} T={t}: max|out|={want.float().abs().max().item():.3f}", flush=True)
         assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        # the same layer without the narrow kernels (256x256 tiles only)
+        saved = hk.tk_kernel.get_narrow()
+        wide = torch.full((t, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+        try:
+            hk.tk_kernel.set_narrow(0, saved[1], saved[2])
+            _forward(lib, w, tok, mode, t, wide)
+            torch.cuda.synchronize()
+        finally:
+            hk.tk_kernel.set_narrow(*saved)
+        assert torch.equal(got.view(torch.int16), wide.view(torch.int16))
 
 
 def test_noalloc_rejects_layers_beyond_the_scratch(hk, lib):
