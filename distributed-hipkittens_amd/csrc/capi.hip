@@ -252,6 +252,28 @@ NarrowConfig narrow_config() {
   return narrow_config_ref();
 }
 
+// Tile blocks of the grouped GEMMs: 2^b M tiles x 32 / 2^b N tiles share an
+// XCD's L2.  2^b = HKMOE_BLOCK_M1 (GEMM 1) / HKMOE_BLOCK_M2 (GEMM 2) from the
+// environment (1, 2, 4, 8, 16 or 32; read once; other values give the
+// default), default 2 M tiles x 16 N tiles: a block then spans one or two
+// experts, whose N tiles share the A rows.  A measurement knob for the L2-miss
+// traffic of other block shapes.
+int block_m_log2(int gemm) {
+  static const int b1 = [] {
+    const int m = env_int("HKMOE_BLOCK_M1", 2);
+    for (int t = 0; t <= 5; ++t)
+      if (m == (1 << t)) return t;
+    return 1;
+  }();
+  static const int b2 = [] {
+    const int m = env_int("HKMOE_BLOCK_M2", 2);
+    for (int t = 0; t <= 5; ++t)
+      if (m == (1 << t)) return t;
+    return 1;
+  }();
+  return gemm == 1 ? b1 : b2;
+}
+
 // Per-device auxiliary stream (default priority, non-blocking) and fork/join
 // events of the one-call layer.  Created on the first call that is not being
 // captured into a graph; the mutex keeps fork/join sequences of concurrent
@@ -579,7 +601,7 @@ static int grouped_gemm1_impl(const void* x, const float* x_scale, const int32_t
   p.n_tiles = inter / 128;
   p.b_packed = w_layout == HKMOE_W_PACKED;
   p.mtile_list = mtile_list;
-  p.blk_m_log2 = 1;  // 2 x 16 tile blocks
+  p.blk_m_log2 = block_m_log2(1);  // 2 x 16 tile blocks by default
   p.tile_ctr = tile_counters;
   p.narrow_cnt = narrow_cnt;
   p.yield_from = yield_from;
@@ -679,7 +701,7 @@ static int grouped_gemm2_impl(const void* hq, const float* hs, const void* w2, c
   p.n_tiles = hidden / kBN;
   p.b_packed = w_layout == HKMOE_W_PACKED;
   p.mtile_list = mtile_list;
-  p.blk_m_log2 = 1;  // 2 x 16 tile blocks
+  p.blk_m_log2 = block_m_log2(2);  // 2 x 16 tile blocks by default
   p.tile_ctr = tile_counters;
   p.narrow_cnt = narrow_cnt;
   p.yield_from = yield_from;
@@ -1248,7 +1270,7 @@ int hkmoe_grouped_gemm1_mx(const void* x, const void* x_words, const int32_t* ga
   p.n_tiles = inter / 128;
   p.b_packed = w_layout == HKMOE_W_PACKED;
   p.mtile_list = mtile_list;
-  p.blk_m_log2 = 1;  // 2 x 16 tile blocks
+  p.blk_m_log2 = block_m_log2(1);  // 2 x 16 tile blocks by default
   p.tile_ctr = tile_counters;
   auto st = static_cast<hipStream_t>(stream);
   return out_format == HKMOE_E4M3 ? launch_gemm<Epi::kSiluMx, Scale::kMX>(p, st)
@@ -1290,7 +1312,7 @@ int hkmoe_grouped_gemm2_mx(const void* hq, const void* hq_words, const void* w2,
   p.n_tiles = hidden / kBN;
   p.b_packed = w_layout == HKMOE_W_PACKED;
   p.mtile_list = mtile_list;
-  p.blk_m_log2 = 1;
+  p.blk_m_log2 = block_m_log2(2);
   p.tile_ctr = tile_counters;
   return launch_gemm<Epi::kStoreBf16, Scale::kMX>(p, static_cast<hipStream_t>(stream));
 }

@@ -193,11 +193,15 @@ __device__ __forceinline__ float silu(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
 }
 
-// Tile row of activation-scale slot s: the lane with l16 = r % 16 of wave-row
-// r / 128 reads its 8 sub-tile scales as 8 consecutive floats.
+// Tile row of activation-scale slot s.  A group's 128 slots are two runs of
+// 64: slots 4*l16 .. 4*l16 + 3 of the first run hold the scales of rows l16,
+// 16 + l16, 32 + l16, 48 + l16 (sub-tiles 0-3 of the lane with that l16), the
+// second run those of sub-tiles 4-7.  Each memory phase then reads one 16-byte
+// chunk per l16 from 256 consecutive bytes: no two of the 16 addresses share a
+// bank (the earlier 8-float runs put l16 and l16 + 8 in the same banks).
 __device__ __forceinline__ int scale_slot_row(int slot) {
   const int wm = slot >> 7, w = slot & 127;
-  return wm * 128 + (w & 7) * 16 + (w >> 3);
+  return wm * 128 + ((w >> 6) * 4 + (w & 3)) * 16 + ((w & 63) >> 2);
 }
 
 // Scaled MFMA with e8m0 operand scales: byte OPB of sb scales the B fragment
@@ -673,7 +677,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         // this step's scales of sub-tiles 0-3 (4-7 in the second memory phase);
         // the factors are formed in the compute phases
         const f32x4 s_lo = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(sb + kTileBytes) +
-                                                           wave_row0 + l16 * 8);
+                                                           wave_row0 + l16 * 4);
         sa_cur[0] = s_lo.x; sa_cur[1] = s_lo.y; sa_cur[2] = s_lo.z; sa_cur[3] = s_lo.w;
         if constexpr (kSilu) {
           sb_cur0 = bsl[kt];
@@ -757,7 +761,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       // ahead (the next tile's B(0) / B(1) at the last two steps)
       if constexpr (kBlockSc) {
         const f32x4 s_hi = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(sb + kTileBytes) +
-                                                           wave_row0 + l16 * 8 + 4);
+                                                           wave_row0 + 64 + l16 * 4);
         sa_cur[0] = s_hi.x; sa_cur[1] = s_hi.y; sa_cur[2] = s_hi.z; sa_cur[3] = s_hi.w;
       }
       if (live_sub > 4) {
