@@ -60,6 +60,17 @@ __device__ __forceinline__ void load_lds_4B(i32x4 rsrc, void* lds_base, int voff
                          4, voffset, soffset, 0, 0);
 }
 
+// 16-byte buffer store: lane stores `v` at rsrc + voffset; stores at offsets
+// past the descriptor's num_records are dropped by the hardware, so a
+// descriptor bounded at the last valid row makes a tile's row stores
+// unconditional (no branch around each store).
+extern "C" __device__ void hk_raw_buffer_store_v4i32(i32x4 data, i32x4 rsrc, int voffset, int soffset,
+                                                     int aux) __asm("llvm.amdgcn.raw.buffer.store.v4i32");
+__device__ __forceinline__ void store_16B(i32x4 rsrc, int voffset, uint4 v) {
+  const i32x4 d = {static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+  hk_raw_buffer_store_v4i32(d, rsrc, voffset, 0, 0);
+}
+
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Buffer offset row * stride + add in unsigned 32-bit arithmetic (the buffer

@@ -858,6 +858,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
     // fragment-shaped writes and the row-shaped reads spread over the banks.
     uint8_t* ct = smem + ((gstep + k_steps - 1) & 1) * kStg;
     const int row0 = cur.row0, valid = cur.valid, nt = cur.nt;
+    // output rows row0 .. row0 + valid - 1 as one buffer: stores to rows past
+    // `valid` (the next expert's rows) fall outside it and are dropped
+    constexpr int kOutBytes = (EPI == Epi::kStoreBf16) ? 2 : (EPI == Epi::kSiluQuant || EPI == Epi::kSiluMx) ? 1 : 4;
+    const i32x4 out_srd =
+        make_srd(static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0) * p.n_out * kOutBytes,
+                 static_cast<uint32_t>(valid) * static_cast<uint32_t>(p.n_out) * kOutBytes);
     // lane position recomputed here, so its address terms are not kept live
     // from the kernel's start
     const int eln = lane_here(), el16 = eln & 15, elg = eln >> 4;
@@ -886,15 +892,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
           }
         }
         sync_lds();
+        // the four LDS reads, then four unconditional stores through a
+        // descriptor that ends at the tile's last valid row (the hardware drops
+        // the rows past it): the reads' latencies overlap, and no branch
+        // separates them from the stores
+        uint4 sv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int idx = wave * 64 + eln + kThreads * u, rr = idx >> 5, c = idx & 31;
+          sv[u] = *reinterpret_cast<const uint4*>(ct + rr * 512 + ((c ^ (rr & 31)) << 4));
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int idx = wave * 64 + eln + kThreads * u, rr = idx >> 5, c = idx & 31;
           const int r = (rr >> 5) * 128 + 32 * q + (rr & 31);
-          if (r < valid) {
-            const uint4 v = *reinterpret_cast<const uint4*>(ct + rr * 512 + ((c ^ (rr & 31)) << 4));
-            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out +
-                                      nt * kBN + c * 8) = v;
-          }
+          store_16B(out_srd, (r * p.n_out + nt * kBN + c * 8) * 2, sv[u]);
         }
         sync_lds();
       }
@@ -1031,14 +1043,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
           }
         }
         sync_lds();
+        uint4 sv[4];  // reads first, then bounded stores, as in the bf16 store
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int idx = wave * 64 + eln + kThreads * u, r = idx >> 3, c = idx & 7;
-          if (r < valid) {
-            const uint4 v = *reinterpret_cast<const uint4*>(ct + r * 128 + ((c ^ (r & 7)) << 4));
-            *reinterpret_cast<uint4*>(static_cast<uint8_t*>(p.c) + static_cast<int64_t>(row0 + r) * p.n_out +
-                                      nt * 128 + c * 16) = v;
-          }
+          sv[u] = *reinterpret_cast<const uint4*>(ct + r * 128 + ((c ^ (r & 7)) << 4));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int idx = wave * 64 + eln + kThreads * u, r = idx >> 3, c = idx & 7;
+          store_16B(out_srd, r * p.n_out + nt * 128 + c * 16, sv[u]);
         }
         sync_lds();  // ct is the next tile's A(1) stage
       }
