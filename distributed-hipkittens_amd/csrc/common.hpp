@@ -60,15 +60,37 @@ __device__ __forceinline__ void load_lds_4B(i32x4 rsrc, void* lds_base, int voff
                          4, voffset, soffset, 0, 0);
 }
 
+// 16 bytes loaded / stored non-temporally (data touched once: the L2 does not
+// keep it at the expense of data that is reused).
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+  const i32x4 v = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+  return uint4{static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y), static_cast<uint32_t>(v.z),
+               static_cast<uint32_t>(v.w)};
+}
+__device__ __forceinline__ void st_nt8(void* p, uint2 v) {
+  typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+  const i32x2 d = {static_cast<int>(v.x), static_cast<int>(v.y)};
+  __builtin_nontemporal_store(d, reinterpret_cast<i32x2*>(p));
+}
+__device__ __forceinline__ void st_nt16(void* p, uint4 v) {
+  const i32x4 d = {static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+  __builtin_nontemporal_store(d, reinterpret_cast<i32x4*>(p));
+}
+
+// Cache-policy operand of the buffer intrinsics on gfx950: bit 0 = sc0,
+// bit 1 = nt (non-temporal: the line is not expected to be reused), bit 4 = sc1.
+constexpr int kAuxNT = 2;
+
 // 16-byte buffer store: lane stores `v` at rsrc + voffset; stores at offsets
 // past the descriptor's num_records are dropped by the hardware, so a
 // descriptor bounded at the last valid row makes a tile's row stores
 // unconditional (no branch around each store).
 extern "C" __device__ void hk_raw_buffer_store_v4i32(i32x4 data, i32x4 rsrc, int voffset, int soffset,
                                                      int aux) __asm("llvm.amdgcn.raw.buffer.store.v4i32");
+template <int AUX = 0>
 __device__ __forceinline__ void store_16B(i32x4 rsrc, int voffset, uint4 v) {
   const i32x4 d = {static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-  hk_raw_buffer_store_v4i32(d, rsrc, voffset, 0, 0);
+  hk_raw_buffer_store_v4i32(d, rsrc, voffset, 0, AUX);
 }
 
 __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

@@ -895,7 +895,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         // the four LDS reads, then four unconditional stores through a
         // descriptor that ends at the tile's last valid row (the hardware drops
         // the rows past it): the reads' latencies overlap, and no branch
-        // separates them from the stores
+        // separates them from the stores.  The output is not read again by
+        // this kernel: non-temporal stores leave the L2 to the operand panels.
         uint4 sv[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -906,7 +907,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
         for (int u = 0; u < 4; ++u) {
           const int idx = wave * 64 + eln + kThreads * u, rr = idx >> 5, c = idx & 31;
           const int r = (rr >> 5) * 128 + 32 * q + (rr & 31);
-          store_16B(out_srd, (r * p.n_out + nt * kBN + c * 8) * 2, sv[u]);
+          store_16B<kAuxNT>(out_srd, (r * p.n_out + nt * kBN + c * 8) * 2, sv[u]);
         }
         sync_lds();
       }
@@ -1052,7 +1053,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int idx = wave * 64 + eln + kThreads * u, r = idx >> 3, c = idx & 7;
-          store_16B(out_srd, r * p.n_out + nt * 128 + c * 16, sv[u]);
+          store_16B<kAuxNT>(out_srd, r * p.n_out + nt * 128 + c * 16, sv[u]);
         }
         sync_lds();  // ct is the next tile's A(1) stage
       }

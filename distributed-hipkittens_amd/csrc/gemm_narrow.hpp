@@ -321,8 +321,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
     load_lds_16B(a_srd, st + 8 * wave * kBK, L.a_voff, ktu * kBK);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      wr[j].lo = hk_raw_buffer_load_v4i32(srd, wvoff[2 * j], ktu * kstride, 0);
-      wr[j].hi = hk_raw_buffer_load_v4i32(srd, wvoff[2 * j + 1], ktu * kstride, 0);
+      // weights are read once: non-temporal loads keep them from displacing
+      // the 256x256 kernel's operand panels in the XCD's L2
+      wr[j].lo = hk_raw_buffer_load_v4i32(srd, wvoff[2 * j], ktu * kstride, kAuxNT);
+      wr[j].hi = hk_raw_buffer_load_v4i32(srd, wvoff[2 * j + 1], ktu * kstride, kAuxNT);
     }
   };
 
@@ -461,7 +463,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
             uint2 v;
             v.x = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
             v.y = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
-            *reinterpret_cast<uint2*>(yrow + 16 * j) = v;
+            st_nt8(yrow + 16 * j, v);  // not read again by this kernel
           }
         }
       }
@@ -508,7 +510,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
                                  quot_e4m3(bf16_bits_to_f32(hi >> 16), qs));
           }
           uint8_t* dst = static_cast<uint8_t*>(p.c) + static_cast<int64_t>(C.row0 + r) * p.n_out + C.nt * 128 + q * 8;
-          *reinterpret_cast<uint2*>(dst) = uint2{qw[0], qw[1]};
+          st_nt8(dst, uint2{qw[0], qw[1]});
           if (q == 0) p.c_scale[static_cast<int64_t>(C.nt) * p.rows + C.row0 + r] = sc;
         }
       }

@@ -422,6 +422,8 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
 //    host sizes the workgroup so the row's 16-byte chunks divide evenly).  The
 //    token's weights and y rows are staged in LDS once; the y loads of up to
 //    8 slots are issued together, then summed in slot order j = 0 .. k-1.
+//    Every y byte is read once and every out byte written once: non-temporal
+//    loads and stores (181 vs 208 us on config 3).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const float* __restrict__ topk_w,
@@ -444,7 +446,7 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t* __restrict
 #pragma unroll
       for (int u = 0; u < 8; ++u)
         if (j0 + u < top_k)
-          v[u] = *reinterpret_cast<const uint4*>(y + static_cast<int64_t>(s_row[j0 + u]) * hidden + c * 8);
+          v[u] = ld_nt16(y + static_cast<int64_t>(s_row[j0 + u]) * hidden + c * 8);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         if (j0 + u < top_k) {
@@ -463,7 +465,7 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t* __restrict
     o.y = pack_bf16x2(acc[2], acc[3]);
     o.z = pack_bf16x2(acc[4], acc[5]);
     o.w = pack_bf16x2(acc[6], acc[7]);
-    *reinterpret_cast<uint4*>(out + t * hidden + c * 8) = o;
+    st_nt16(out + t * hidden + c * 8, o);
   }
 }
 
