@@ -1113,15 +1113,19 @@ def main():
                                 "threshold" if narrow else "grouped_gemm1 (gate/up + SiLU*up)"),
                      "achieved": round(g1_tflops, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(g1_tflops / PEAK_FP8_TFLOPS, 4), "traffic": traffic,
-                     "avg_ms": round(ms["grouped_gemm1"], 4), "flops_per_launch": g1_flops},
+                     "avg_ms": round(ms.get("grouped_gemm1", 0.0), 4), "flops_per_launch": g1_flops},
         "settle": settle,
         "kernels_ms": {k: round(v, 4) for k, v in ms.items()},
         "kernel_timing": {k: v for k, v in kt.items() if k != "kernels_ms"},
-        "gemm_only_tflops": round(flops / ((ms["grouped_gemm1"] + ms["grouped_gemm2"]) * 1e-3) / 1e12, 2),
     }
+    if "grouped_gemm1" in ms and "grouped_gemm2" in ms:
+        res["gemm_only_tflops"] = round(flops / ((ms["grouped_gemm1"] + ms["grouped_gemm2"]) * 1e-3) / 1e12, 2)
     if narrow:
         # narrow kernels stream the small experts' weights: HBM-bound
         cus, max_rows, share = narrow_setting(inp)
+        # with every expert narrow (T <= max_rows) no 256x256 GEMM is launched:
+        # GEMM 1's span is the narrow kernel's
+        g1_span = kt.get("gemm1_span_ms", ms["narrow_gemm1"])
         nb1 = n_narrow * 2 * cfg["I"] * cfg["H"]
         nb2 = n_narrow * cfg["H"] * cfg["I"]
         res["narrow"] = {
@@ -1130,8 +1134,8 @@ def main():
                       "GB_s": round(nb1 / ms["narrow_gemm1"] / 1e6, 1)},
             "gemm2": {"ms": round(ms["narrow_gemm2"], 4), "weight_bytes": nb2,
                       "GB_s": round(nb2 / ms["narrow_gemm2"] / 1e6, 1)},
-            "gemm1_span_ms": round(kt["gemm1_span_ms"], 4),
-            "gemm1_span_tflops": round(2.0 * rows * 2 * cfg["I"] * cfg["H"] / (kt["gemm1_span_ms"] * 1e-3) / 1e12, 2),
+            "gemm1_span_ms": round(g1_span, 4),
+            "gemm1_span_tflops": round(2.0 * rows * 2 * cfg["I"] * cfg["H"] / (g1_span * 1e-3) / 1e12, 2),
         }
         if narrow_rows == rows:
             # every expert is narrow (decode-like): the dominant kernel is the
@@ -1140,7 +1144,7 @@ def main():
                                "achieved": round(nb1 / ms["narrow_gemm1"] / 1e6, 1), "peak": PEAK_HBM_GBS,
                                "unit": "GB/s", "frac": round(nb1 / ms["narrow_gemm1"] / 1e6 / PEAK_HBM_GBS, 4),
                                "traffic": None, "avg_ms": round(ms["narrow_gemm1"], 4), "bytes_per_launch": nb1}
-        res.pop("gemm_only_tflops")
+        res.pop("gemm_only_tflops", None)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(inp, cfg, args.cpu_seconds)
     if args.config == "dsv3" and args.other_configs:

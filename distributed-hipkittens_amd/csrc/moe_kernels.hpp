@@ -125,10 +125,14 @@ __global__ __launch_bounds__(kTopkThreads) void route_topk_kernel(
 //     most of its time waiting for them).
 //  b. expert_offsets: one workgroup of 1024 threads, thread = expert: scans
 //     over experts (offsets, M-tile offsets), the M-tile list, counters.
+// With at most kOffFuseBlocks routing blocks (decode-sized batches) the
+// expert_offsets thread of each expert also does (a) itself, reading the few
+// counts in one pass: one launch instead of two.
 // ---------------------------------------------------------------------------
 constexpr int kOffExperts = 16;                        // experts per block-scan workgroup
 constexpr int kOffParts = kScanThreads / kOffExperts;  // block ranges per expert
 constexpr int kOffCache = 32;                          // counts a thread keeps in registers
+constexpr int kOffFuseBlocks = 16;                     // routing blocks done by expert_offsets
 
 __global__ __launch_bounds__(kScanThreads) void expert_block_scan_kernel(
     const int32_t* __restrict__ block_counts, int nblk, int num_experts, int32_t* __restrict__ counts,
@@ -234,13 +238,32 @@ __device__ __forceinline__ void block_exclusive_scan_n(int (&v)[N], int (*wave_t
 }
 
 __global__ __launch_bounds__(kScanThreads) void expert_offsets_kernel(
-    int num_experts, const int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int num_experts, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ mtile_offsets, int32_t* __restrict__ mtile_list, int tile_m,
-    float* amax_reset, int32_t* tile_counters, int narrow_max, int32_t* narrow_info) {
+    float* amax_reset, int32_t* tile_counters, int narrow_max, int32_t* narrow_info,
+    const int32_t* __restrict__ block_counts, int fused_nblk, int32_t* __restrict__ block_base) {
   __shared__ int wave_tot[kScanThreads / 64][5];
   __shared__ int n_head, n_tail;
   const int e = threadIdx.x;  // E <= kScanThreads
-  const int cnt = (e < num_experts) ? counts[e] : 0;
+  int cnt = 0;
+  if (fused_nblk >= 0) {
+    // fused_nblk (<= kOffFuseBlocks) routing blocks: this expert's prefix over
+    // them and its total, as expert_block_scan_kernel computes them (-1: the
+    // block scan ran before)
+    if (e < num_experts) {
+      int c[kOffFuseBlocks];
+#pragma unroll
+      for (int b = 0; b < kOffFuseBlocks; ++b) c[b] = b < fused_nblk ? block_counts[b * num_experts + e] : 0;
+#pragma unroll
+      for (int b = 0; b < kOffFuseBlocks; ++b) {
+        if (b < fused_nblk) block_base[b * num_experts + e] = cnt;
+        cnt += c[b];
+      }
+      counts[e] = cnt;
+    }
+  } else if (e < num_experts) {
+    cnt = counts[e];
+  }
   const int mt = (cnt + tile_m - 1) / tile_m;
   // M-tile list [(expert, first row)]: first the experts with at least one
   // full tile, each with all its tiles (full ones, then its partial one), in

@@ -20,11 +20,15 @@ def _layer(hk, block, T=300, seed=5):
     return layer, g
 
 
-@pytest.mark.parametrize("block", [True, False])
-def test_timed_calls_match_untimed(hk, block):
+@pytest.mark.parametrize("block,T", [(True, 300), (False, 300), (True, 1000), (True, 64)])
+def test_timed_calls_match_untimed(hk, block, T):
+    """T=300: 10 routing blocks (the block scan runs inside expert_offsets) and,
+    with block scales, T*k <= 2*E*64: the one-stream narrow schedule.  T=1000:
+    32 blocks (separate block scan) and the two-stream schedule.  T=64: every
+    expert has at most 64 rows, so only the narrow GEMMs are launched."""
     tk = hk.tk_kernel
     roles = tk.TIMING_ROLES
-    layer, g = _layer(hk, block)
+    layer, g = _layer(hk, block, T=T)
     want = layer(g["x_q"], g["x_scale"], g["logits"])
     torch.cuda.synchronize()
     tk.kernel_timing(3)
@@ -36,25 +40,38 @@ def test_timed_calls_match_untimed(hk, block):
         tk.kernel_timing(0)
     for o in outs:
         assert torch.equal(o.view(torch.int16), want.view(torch.int16))
+    k, e = 4, 16
+    fused_scan = tk.route_blocks(T) <= 16
+    all_narrow = block and T <= 64
+    one_stream = block and T * k <= 2 * e * 64
     for tl in sets:
         got = {roles[i]: v for i, v in enumerate(tl) if v[0] >= 0}
-        print(f"block={block} timeline (ms): {got}", flush=True)
-        for name in ("route_topk", "expert_block_scan", "expert_offsets", "scatter", "grouped_gemm1",
-                     "grouped_gemm2", "combine"):
+        print(f"block={block} T={T} timeline (ms): {got}", flush=True)
+        expect = ["route_topk", "expert_offsets", "scatter", "combine"]
+        expect += [] if all_narrow else ["grouped_gemm1", "grouped_gemm2"]
+        expect += ["narrow_gemm1", "narrow_gemm2"] if block else []
+        for name in expect:
             assert name in got, name
+        assert ("expert_block_scan" in got) == (not fused_scan)
+        if all_narrow:
+            assert "grouped_gemm1" not in got and "grouped_gemm2" not in got
         assert got["route_topk"][0] == 0.0
-        for b, e in got.values():
-            assert 0.0 <= b < e < 1000.0
+        for b, e_ in got.values():
+            assert 0.0 <= b < e_ < 1000.0
         main = [n for n in ("route_topk", "expert_block_scan", "expert_offsets", "scatter", "grouped_gemm1",
                             "requant", "grouped_gemm2", "combine") if n in got]
         for a, b in zip(main, main[1:]):
             assert got[a][1] <= got[b][0] + 1e-3, (a, b)
         assert ("requant" in got) == (not block)
-        if block:
-            # T*k = 1200 <= 2*E*64: the one-stream narrow schedule, after each 256x256 GEMM
-            assert got["grouped_gemm1"][1] <= got["narrow_gemm1"][0] + 1e-3
-            assert got["narrow_gemm1"][1] <= got["grouped_gemm2"][0] + 1e-3
-            assert got["grouped_gemm2"][1] <= got["narrow_gemm2"][0] + 1e-3
+        if one_stream:
+            # after each 256x256 GEMM (when there is one), on the caller's stream
+            seq = [n for n in ("grouped_gemm1", "narrow_gemm1", "grouped_gemm2", "narrow_gemm2", "combine")
+                   if n in got]
+            for a, b in zip(seq, seq[1:]):
+                assert got[a][1] <= got[b][0] + 1e-3, (a, b)
+        elif block:
+            # beside the 256x256 GEMM 1 on the auxiliary stream, joined before the combine
+            assert got["narrow_gemm1"][0] < got["grouped_gemm1"][1]
             assert got["narrow_gemm2"][1] <= got["combine"][0] + 1e-3
 
 
