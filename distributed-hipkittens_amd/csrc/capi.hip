@@ -682,6 +682,7 @@ static int grouped_gemm2_impl(const void* hq, const float* hs, const void* w2, c
   HK_REQUIRE(inter > 0 && inter % kGroup == 0 && inter <= kGroup * kMaxKBlocks,
              "grouped_gemm2: inter=%d must be a multiple of 128 and <= %d", inter, kGroup * kMaxKBlocks);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm2: bad rows");
+  HK_REQUIRE(rows * inter < (1ll << 32), "grouped_gemm2: rows*inter must be < 2^32 (32-bit buffer offsets into hq)");
   HK_REQUIRE(static_cast<int64_t>(hidden) * inter < (1ll << 32), "grouped_gemm2: expert weight too large");
   HK_REQUIRE(scale_mode == HKMOE_SCALE_TENSOR || scale_mode == HKMOE_SCALE_BLOCK,
              "grouped_gemm2: bad scale_mode %d", scale_mode);
@@ -920,7 +921,13 @@ static int moe_forward_impl(const void* x_q, const float* x_scale, const float* 
   HK_REQUIRE(top_k >= 1 && top_k <= num_experts && top_k <= kMaxTopK, "moe_forward: bad top_k=%d", top_k);
   HK_REQUIRE(hidden > 0 && hidden % kBN == 0 && hidden <= kGroup * kMaxKBlocks,
              "moe_forward: hidden=%d must be a multiple of 256 and <= %d", hidden, kGroup * kMaxKBlocks);
-  HK_REQUIRE(inter > 0 && inter % 128 == 0, "moe_forward: inter=%d must be a multiple of 128", inter);
+  HK_REQUIRE(inter > 0 && inter % 128 == 0 && inter <= kGroup * kMaxKBlocks,
+             "moe_forward: inter=%d must be a multiple of 128 and <= %d", inter, kGroup * kMaxKBlocks);
+  // every operand of the grouped GEMMs is addressed by 32-bit buffer offsets:
+  // checked here, before any kernel of the layer is launched
+  HK_REQUIRE(2ll * inter * hidden < (1ll << 32), "moe_forward: expert weight too large (2*I*H must be < 2^32)");
+  HK_REQUIRE(num_tokens * hidden < (1ll << 32) && num_tokens * top_k * inter < (1ll << 32),
+             "moe_forward: T*H and T*k*I must be < 2^32 (32-bit buffer offsets)");
   if (num_tokens == 0) return HKMOE_OK;
   const bool block = scale_mode == HKMOE_SCALE_BLOCK;
   const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, scale_mode);
@@ -1300,6 +1307,7 @@ int hkmoe_grouped_gemm2_mx(const void* hq, const void* hq_words, const void* w2,
   HK_REQUIRE(inter > 0 && inter % kGroup == 0 && inter <= kGroup * kMaxKBlocks,
              "grouped_gemm2_mx: inter=%d must be a multiple of 128 and <= %d", inter, kGroup * kMaxKBlocks);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31), "grouped_gemm2_mx: bad rows");
+  HK_REQUIRE(rows * inter < (1ll << 32), "grouped_gemm2_mx: rows*inter must be < 2^32 (32-bit buffer offsets into hq)");
   HK_REQUIRE(static_cast<int64_t>(hidden) * inter < (1ll << 32), "grouped_gemm2_mx: expert weight too large");
   HK_REQUIRE(w_layout == HKMOE_W_ROWS || w_layout == HKMOE_W_PACKED, "grouped_gemm2_mx: bad w_layout %d",
              w_layout);
@@ -1346,6 +1354,9 @@ int hkmoe_moe_forward_mx(const void* x_q, const void* x_e8m0, const float* logit
              "moe_forward_mx: hidden=%d must be a multiple of 256 and <= %d", hidden, kGroup * kMaxKBlocks);
   HK_REQUIRE(inter > 0 && inter % 128 == 0 && inter <= kGroup * kMaxKBlocks,
              "moe_forward_mx: inter=%d must be a multiple of 128 and <= %d", inter, kGroup * kMaxKBlocks);
+  HK_REQUIRE(2ll * inter * hidden < (1ll << 32), "moe_forward_mx: expert weight too large (2*I*H must be < 2^32)");
+  HK_REQUIRE(num_tokens * hidden < (1ll << 32) && num_tokens * top_k * inter < (1ll << 32),
+             "moe_forward_mx: T*H and T*k*I must be < 2^32 (32-bit buffer offsets)");
   if (num_tokens == 0) return HKMOE_OK;
   const MoeWorkspace need = carve(nullptr, num_tokens, num_experts, top_k, hidden, inter, HKMOE_SCALE_MX);
   if (workspace == nullptr || workspace_bytes < need.bytes)

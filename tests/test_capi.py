@@ -110,6 +110,22 @@ def test_moe_forward_argument_errors(lib):
     args[10] = i32(4000)  # hidden not a multiple of 256
     assert lib.hkmoe_moe_forward(*args) == 1
     assert "hidden=4000" in _err(lib)
+    args[10] = i32(4096)
+    args[11] = i32(16512)  # I beyond GEMM 2's 128 K steps: refused before any launch
+    assert lib.hkmoe_moe_forward(*args) == 1
+    assert "inter=16512" in _err(lib)
+    # hq = T*k rows of I bytes past 4 GiB cannot be addressed by 32-bit buffer
+    # offsets: refused before any launch (T*k*I = 2^19 * 8 * 1024 = 2^32)
+    args[7], args[8], args[9], args[11] = i64(1 << 19), i32(64), i32(8), i32(1024)
+    assert lib.hkmoe_moe_forward(*args) == 1
+    assert "T*k*I" in _err(lib)
+    mx = args[:12] + [0, fake, fake, ctypes.c_size_t(1 << 40), None]
+    assert lib.hkmoe_moe_forward_mx(*mx) == 1
+    assert "T*k*I" in _err(lib)
+    # the same bound on the stepwise GEMM 2 (rows*I = 2^22 * 1024)
+    rc = lib.hkmoe_grouped_gemm2(fake, fake, fake, fake, fake, fake, None, i64(1 << 22), i32(8), i32(256),
+                                 i32(1024), 1, 0, fake, None, None)
+    assert rc == 1 and "rows*inter" in _err(lib)
 
 
 def test_moe_forward_empty_batch(lib):
