@@ -93,13 +93,20 @@ void hk_launch(void (*kern)(Kargs...), dim3 grid, dim3 block, uint32_t lds, hipS
 }
 
 // Marks the launches of one layer call as timed (a set of the ring) for its
-// lifetime; does nothing while timing is off or on another device.
+// lifetime; does nothing while timing is off or on another device.  A timed
+// call holds the timing mutex until it has enqueued its last launch, so
+// timing_events never sees the ring replaced by a concurrent
+// hkmoe_kernel_timing, and timed calls from several host threads take their
+// sets one after the other.
 struct TimedCall {
   bool on = false;
-  TimedCall() {
-    std::lock_guard<std::mutex> g(g_timing_mu);
+  std::unique_lock<std::mutex> lk;
+  TimedCall() : lk(g_timing_mu) {
     int dev = -1;
-    if (g_timing.calls <= 0 || hipGetDevice(&dev) != hipSuccess || dev != g_timing.device) return;
+    if (g_timing.calls <= 0 || hipGetDevice(&dev) != hipSuccess || dev != g_timing.device) {
+      lk.unlock();
+      return;
+    }
     t_slot = g_timing.next;
     g_timing.next = (g_timing.next + 1) % g_timing.calls;
     std::fill_n(g_timing.used.begin() + static_cast<size_t>(t_slot) * HKMOE_TIMING_ROLES, HKMOE_TIMING_ROLES, 0);
