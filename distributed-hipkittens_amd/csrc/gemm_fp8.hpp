@@ -274,6 +274,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   constexpr bool kSilu = (EPI == Epi::kSiluBf16 || EPI == Epi::kSiluQuant || EPI == Epi::kSiluMx);
   // stage: A tile, B tile, A scales (1 KiB) and, in MX mode, B scales (1 KiB)
   constexpr int kStg = kMX ? kStageBytes + kScaleBytes : kStageBytes;
+  // A sub-tiles of the first compute phase that it reads itself instead of
+  // the first memory phase (block scales): that phase is bound by its LDS
+  // reads (17 ds_read_b128 per wave against 9 in the second), while in the
+  // compute phase the reads overlap the MFMAs and the other wave's memory
+  // phase.  Sub-tiles 2 and 3 are read after MFMAs 1 and 5, in time for
+  // their first use at MFMAs 8 and 12 (layer -0.3%; three sub-tiles: the same).
+  constexpr int kLateA = kBlockSc ? 2 : 0;
   static_assert(EPI != Epi::kSiluMx || kMX, "MX requantisation needs MX scales");
   static_assert(2 * kStg <= kBsOff, "LDS budget");
 
@@ -671,7 +678,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
       }
       if (live_sub > 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = read_operand<kMX>(sa, wave_row0 + i * 16 + l16, lg, fx);
+        for (int i = 0; i < 4 - kLateA; ++i) af[i] = read_operand<kMX>(sa, wave_row0 + i * 16 + l16, lg, fx);
       }
       if constexpr (kBlockSc) {
         // this step's scales of sub-tiles 0-3 (4-7 in the second memory phase);
@@ -730,6 +737,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 #pragma unroll
             for (int t = 0; t < 18; ++t) {
               if (t < 16) pr[t % 3] = mfma_e4m3_16x16x128(bf[t & 3], af[t >> 2], f32x4{0.f, 0.f, 0.f, 0.f});
+              // the first compute phase reads its last kLateA A sub-tiles here,
+              // a few MFMAs before their first use (sub-tile u at MFMA 4u)
+              if (i0 == 0 && kLateA > 0 && (t == 1 || t == 5) && (t == 5 || kLateA == 2)) {
+                const int u = (t == 1) ? 2 : 3;
+                af[u] = read_operand<kMX>(sa, wave_row0 + u * 16 + l16, lg, fx);
+              }
               if (t >= 2) {
                 const int u = (t - 2) >> 2, j = (t - 2) & 3;
                 if (j == 0) {
@@ -741,6 +754,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
               if (t < 16) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA, then the VALU
               if (t >= 2 && ((t - 2) & 3) == 0) __builtin_amdgcn_sched_group_barrier(0x002, kSilu ? 6 : 5, 0);
               if (t >= 2 && ((t - 2) & 3) != 0) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+              if (i0 == 0 && kLateA > 0 && (t == 1 || t == 5) && (t == 5 || kLateA == 2))
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // its two LDS reads
             }
           } else {
 #pragma unroll
