@@ -250,10 +250,11 @@ __device__ __forceinline__ void b_source(const GemmParams& p, int e, int nt, boo
                                          int& voff, int& kstride) {
   const int lane = lane_here();
   if (p.b_packed) {
-    srd = make_srd(p.b + (static_cast<int64_t>(e) * (p.nb / kBN) + nt) * kBN * p.K,
-                   static_cast<uint32_t>(kBN) * p.K);
+    // K step kt of N tile nt: block (e, kt, nt), nb/256 blocks per K step
+    srd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K + static_cast<int64_t>(nt) * kTileBytes,
+                   static_cast<uint32_t>(static_cast<int64_t>(p.nb) * p.K - static_cast<int64_t>(nt) * kTileBytes));
     voff = wg * 8 * kBK + lane * 16;
-    kstride = kTileBytes;
+    kstride = (p.nb / kBN) * kTileBytes;
   } else {
     srd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K, static_cast<uint32_t>(p.nb) * p.K);
     const int ld_row = 8 * wg + (lane >> 3), ld_chunk = (lane & 7) ^ swz(ld_row);
@@ -1092,11 +1093,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
 #undef HK_BS
 #pragma clang diagnostic pop
 
-// Packed weight layout (a load-time transform; the grouped GEMMs then stream
-// every weight panel sequentially instead of 128 bytes from each of 256 rows
-// 7-14 KiB apart).  For expert e, 256-row N tile nt and K step kt the 32 KiB
-// block at ((e*(nb/256) + nt)*(K/128) + kt)*32 KiB holds the tile's sixteen
-// 16-row MFMA fragments in operand-register order ("fragment-major"):
+// Packed weight layout (a load-time transform; the grouped GEMMs then read
+// each K step of a weight panel as one 32 KiB block instead of 128 bytes from
+// each of 256 rows 7-14 KiB apart).  For expert e, 256-row N tile nt and K
+// step kt the 32 KiB block at ((e*(K/128) + kt)*(nb/256) + nt)*32 KiB holds
+// the tile's sixteen 16-row MFMA fragments in operand-register order
+// ("fragment-major").  The N tiles of one K step are adjacent: the narrow
+// kernels, whose workgroups stream different N tiles of the same experts at
+// about the same K step, read 0.8-2.7% faster than with each N tile's K steps
+// adjacent (same bytes):
 //   block[f*2048 + h*1024 + l*16 + b] = w[e][wrow(16f + l%16)][kt*128 + (2*(l/16) + h)*16 + b],
 // i.e. lane l's registers 0-3 (h = 0) and 4-7 (h = 1) of fragment f, so one
 // 64-lane 16-byte load of 1 KiB contiguous bytes fills one register half of a
@@ -1119,10 +1124,11 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint8_t* __rest
     const int f = in >> 7, h = (in >> 6) & 1, l = in & 63;
     const int R = 16 * f + (l & 15);
     const int chunk = 2 * (l >> 4) + h;
-    const int kt = static_cast<int>(blk % ks);
-    const int64_t tile = blk / ks;
-    const int64_t e = tile / ntile;
-    const int nt = static_cast<int>(tile - e * ntile);
+    // block order (e, kt, nt): the N tiles of one K step are adjacent
+    const int nt = static_cast<int>(blk % ntile);
+    const int64_t ek = blk / ntile;
+    const int kt = static_cast<int>(ek % ks);
+    const int64_t e = ek / ks;
     const int64_t wrow = gate_up ? nt * 128 + 32 * (R >> 6) + (R & 31) + ((R >> 5) & 1) * gate_up
                                  : static_cast<int64_t>(nt) * kBN + R;
     const uint8_t* src = w + (e * nb + wrow) * K + kt * kBK + (chunk << 4);

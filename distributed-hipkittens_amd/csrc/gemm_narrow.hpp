@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
   // (gate) and of the second (up) block row of this wave's columns
   const int ws_voff0 = min(lane, k_steps - 1) * 4;
   const int ws_voff1 = ws_voff0 + (kSilu ? (p.n_out / kGroup) * k_steps * 4 : 0);
-  const int kstride = p.b_packed ? kTileBytes : kBK;
+  const int kstride = p.b_packed ? (p.nb / kBN) * kTileBytes : kBK;
 
   // per-item state of the load side: uniform descriptors, and the lane's
   // A-row and A-scale offsets
@@ -267,8 +267,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_narrow(GemmParams p) {
     C.nt = nt;
     C.mf = (valid + 15) >> 4;
     if (p.b_packed) {
-      L.wsrd = make_srd(p.b + (static_cast<int64_t>(e) * (p.nb / kBN) + nt) * kBN * p.K,
-                        static_cast<uint32_t>(kBN) * p.K);
+      L.wsrd = make_srd(p.b + static_cast<int64_t>(e) * p.nb * p.K + static_cast<int64_t>(nt) * kTileBytes,
+                        static_cast<uint32_t>(static_cast<int64_t>(p.nb) * p.K - static_cast<int64_t>(nt) * kTileBytes));
     } else {
       const int nbase = kSilu ? nt * 128 : nt * kBN;
       L.wsrd = make_srd(p.b + (static_cast<int64_t>(e) * p.nb + nbase) * p.K,

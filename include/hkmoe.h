@@ -229,8 +229,9 @@ int hkmoe_grouped_gemm2_part(const void* hq, const float* hs, const void* w2, co
  * K step becomes one contiguous 32 KiB block holding its sixteen 16-row MFMA
  * fragments in operand-register order (each fragment as two 1 KiB register
  * halves: byte f*2048 + h*1024 + l*16 + b = row 16f + l%16, K byte
- * (2*(l/16) + h)*16 + b), so a tile's weights stream sequentially and every
- * 64-lane load of a register half reads 1 KiB of whole cache lines.  gate_up = I for the fused gate/up
+ * (2*(l/16) + h)*16 + b); block (e, kt, nt) sits at ((e*(K/128) + kt)*(N/256)
+ * + nt)*32 KiB, so every 64-lane load of a register half reads 1 KiB of whole
+ * cache lines and the N tiles of one K step are adjacent.  gate_up = I for the fused gate/up
  * weights of GEMM 1 (N = 2I: rows [gate | up]), 0 otherwise.
  * Requires N % 256 == 0, K % 128 == 0 (gate_up: N == 2*gate_up).
  * No reference counterpart (the reference's GEMMs read [N, K] rows directly);
