@@ -276,12 +276,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
   // stage: A tile, B tile, A scales (1 KiB) and, in MX mode, B scales (1 KiB)
   constexpr int kStg = kMX ? kStageBytes + kScaleBytes : kStageBytes;
   // A sub-tiles of the first compute phase that it reads itself instead of
-  // the first memory phase (block scales): that phase is bound by its LDS
-  // reads (17 ds_read_b128 per wave against 9 in the second), while in the
-  // compute phase the reads overlap the MFMAs and the other wave's memory
-  // phase.  Sub-tiles 2 and 3 are read after MFMAs 1 and 5, in time for
-  // their first use at MFMAs 8 and 12 (layer -0.3%; three sub-tiles: the same).
-  constexpr int kLateA = kBlockSc ? 2 : 0;
+  // the first memory phase (block and per-tensor scales): that phase is bound
+  // by its LDS reads (17 ds_read_b128 per wave against 9 in the second), while
+  // in the compute phase the reads overlap the MFMAs and the other wave's
+  // memory phase.  Sub-tiles 2 and 3 are read after MFMAs 1 and 5, in time for
+  // their first use at MFMAs 8 and 12 (config-3 layer -0.3%, three sub-tiles
+  // the same; Mixtral layer -0.7%; dense GEMMs unchanged).
+  constexpr int kLateA = (kBlockSc || SC == Scale::kTensor) ? 2 : 0;
   static_assert(EPI != Epi::kSiluMx || kMX, "MX requantisation needs MX scales");
   static_assert(2 * kStg <= kBsOff, "LDS budget");
 
@@ -763,6 +764,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_fp8_persistent(GemmParams p)
             for (int t = 0; t < 16; ++t) {
               const int u = t >> 2, j = t & 3;
               acc[i0 + u][j] = mfma_e4m3_16x16x128(bf[j], af[u], acc[i0 + u][j]);
+              if (i0 == 0 && kLateA > 0 && (t == 1 || t == 5) && (t == 5 || kLateA == 2)) {
+                const int ul = (t == 1) ? 2 : 3;
+                af[ul] = read_operand<kMX>(sa, wave_row0 + ul * 16 + l16, lg, fx);
+              }
+              if (kLateA > 0 && i0 == 0) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if ((t == 1 || t == 5) && (t == 5 || kLateA == 2)) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+              }
             }
           }
         }
