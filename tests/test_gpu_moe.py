@@ -119,6 +119,42 @@ def test_moe_single_call_matches_steps(hk, name):
     assert torch.equal(o1.view(torch.int16), out.view(torch.int16))
 
 
+@pytest.mark.parametrize("t,e,k,block", [(1, 8, 2, True), (33, 16, 4, False), (512, 64, 8, True),
+                                         (513, 64, 8, True), (200, 1024, 32, True), (96, 300, 7, False)])
+def test_layer_small_batches_match_steps(hk, t, e, k, block):
+    """The one-call layer (narrow schedule, block scan inside expert_offsets up
+    to 16 routing blocks) against the stepwise path (separate kernels, 256x256
+    GEMMs only), bit for bit: T = 1, 33, 512 (16 routing blocks) and 513, E =
+    1024 (64 experts per lane of a token's top-k row), k = 32, E not a power
+    of two, with and without block scales."""
+    print(f"one-call vs stepwise T={t} E={e} k={k} block={block}", flush=True)
+    # inputs drawn and quantised on the device (E = 1024 weights are slow to
+    # make on the host); both paths see the same tensors
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    x = torch.randn((t, 256), device="cuda", generator=gen)
+    logits = torch.randn((t, e), device="cuda", generator=gen)
+    logits -= 1.1 * torch.log1p(torch.randperm(e, device="cuda", generator=gen).float())  # skewed routing
+    w13 = torch.randn((e, 256, 256), device="cuda", generator=gen)
+    w2 = torch.randn((e, 256, 128), device="cuda", generator=gen)
+    if block:
+        x_q, x_s = hk.quant_group(x)
+        w13_q, w13_s = hk.quant_block(w13)
+        w2_q, w2_s = hk.quant_block(w2)
+    else:
+        x_q, x_s = hk.quant_tensor(x)
+        w13_q, s13 = hk.quant_tensor(w13.reshape(e * 256, 256))
+        w2_q, s2 = hk.quant_tensor(w2.reshape(e * 256, 128))
+        w13_q, w2_q = w13_q.view(e, 256, 256), w2_q.view(e, 256, 128)
+        w13_s, w2_s = s13.expand(e).contiguous(), s2.expand(e).contiguous()
+    g = dict(x_q=x_q, x_scale=x_s, logits=logits, w13_q=w13_q, w13_scale=w13_s, w2_q=w2_q, w2_scale=w2_s,
+             top_k=k)
+    r = _run_steps(hk, g, keep_h=False)
+    out = hk.moe_forward(g["x_q"], g["x_scale"], g["logits"], g["w13_q"], g["w13_scale"],
+                         g["w2_q"], g["w2_scale"], g["top_k"])
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), r["out"].view(torch.int16))
+
+
 @pytest.mark.parametrize("name", ["tensor_e8k2", "block_e16k4_skew"])
 def test_moe_empty_batch(hk, name):
     """T = 0 tokens: the layer returns an empty [0, H] output and launches nothing
