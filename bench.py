@@ -779,6 +779,9 @@ def summarize_profile(args):
     if os.path.exists(tj):
         with open(tj) as f:
             old = json.load(f)
+    # this config's entries are replaced as a whole: kernels the path no longer
+    # launches drop out
+    old = {k: v for k, v in old.items() if not k.startswith(args.config + ":")}
     old.update(traffic)
     with open(tj, "w") as f:
         json.dump(old, f, indent=1, sort_keys=True)
@@ -1140,10 +1143,17 @@ def main():
         if narrow_rows == rows:
             # every expert is narrow (decode-like): the dominant kernel is the
             # narrow GEMM 1, bound by streaming the experts' weights from HBM
+            ntraffic = None
+            if os.path.exists(args.traffic):
+                try:
+                    with open(args.traffic) as f:
+                        ntraffic = json.load(f).get(f"{args.config}:narrow_gemm1")
+                except Exception:
+                    ntraffic = None
             res["roofline"] = {"bound": "hbm", "kernel": "narrow grouped_gemm1 (gate/up + SiLU*up)",
                                "achieved": round(nb1 / ms["narrow_gemm1"] / 1e6, 1), "peak": PEAK_HBM_GBS,
                                "unit": "GB/s", "frac": round(nb1 / ms["narrow_gemm1"] / 1e6 / PEAK_HBM_GBS, 4),
-                               "traffic": None, "avg_ms": round(ms["narrow_gemm1"], 4), "bytes_per_launch": nb1}
+                               "traffic": ntraffic, "avg_ms": round(ms["narrow_gemm1"], 4), "bytes_per_launch": nb1}
         res.pop("gemm_only_tflops", None)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(inp, cfg, args.cpu_seconds)
