@@ -1185,7 +1185,8 @@ def other_configs(args):
         keep = {k: d[k] for k in ("value", "unit", "ms_per_step", "pct_fp8_peak", "eager_ms_per_step") if k in d}
         keep["workload"] = d["config"]["workload"]
         rf = d.get("roofline", {})
-        keep["roofline"] = {k: rf[k] for k in ("kernel", "bound", "achieved", "unit", "frac", "avg_ms") if k in rf}
+        keep["roofline"] = {k: rf[k] for k in ("kernel", "bound", "achieved", "peak", "unit", "frac", "traffic", "avg_ms")
+                            if k in rf}
         out[name] = keep
     return out
 
