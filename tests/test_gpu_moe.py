@@ -155,6 +155,54 @@ def test_layer_small_batches_match_steps(hk, t, e, k, block):
     assert torch.equal(out.view(torch.int16), r["out"].view(torch.int16))
 
 
+def test_layer_concurrent_host_threads(hk):
+    """Two host threads, each with its own layer and its own (default-priority)
+    stream, run the two-stream layer at the same time: their narrow kernels share
+    the library's auxiliary stream and fork/join events, which a lock held over
+    each call's launch sequence keeps apart.  Every output equals the serial
+    result bit for bit."""
+    import threading
+    t, e, k = 1536, 64, 8  # T*k = 12288 > 2*E*64 rows: narrow experts beside 256x256 ones, two streams
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    w13_q, w13_s = hk.quant_block(torch.randn((e, 512, 512), device="cuda", generator=gen))
+    w2_q, w2_s = hk.quant_block(torch.randn((e, 512, 256), device="cuda", generator=gen))
+    batches = []
+    for _ in range(2):
+        x_q, x_s = hk.quant_group(torch.randn((t, 512), device="cuda", generator=gen))
+        logits = torch.randn((t, e), device="cuda", generator=gen)
+        logits -= 1.1 * torch.log1p(torch.randperm(e, device="cuda", generator=gen).float())
+        counts = torch.bincount(torch.topk(logits, k, dim=1).indices.flatten(), minlength=e)
+        assert int(((counts > 0) & (counts <= 64)).sum()) > 0 and int((counts > 256).sum()) > 0
+        batches.append((x_q, x_s, logits))
+    layers = [hk.MoELayer(w13_q, w13_s, w2_q, w2_s, k) for _ in range(2)]
+    refs = [layers[i](*batches[i]).clone() for i in range(2)]
+    torch.cuda.synchronize()
+    outs, errors = [[], []], []
+
+    def run(i):
+        s = torch.cuda.Stream()
+        try:
+            with torch.cuda.stream(s):
+                for _ in range(6):
+                    outs[i].append(layers[i](*batches[i]).clone())
+            s.synchronize()
+        except Exception as ex:  # reported below, in the test's thread
+            errors.append(ex)
+
+    print(f"concurrent layers T={t} E={e} k={k}, two host threads", flush=True)
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads), "a layer thread did not finish"
+    assert not errors, errors
+    for i in range(2):
+        assert len(outs[i]) == 6
+        for o in outs[i]:
+            assert torch.equal(o.view(torch.int16), refs[i].view(torch.int16))
+
+
 @pytest.mark.parametrize("name", ["tensor_e8k2", "block_e16k4_skew"])
 def test_moe_empty_batch(hk, name):
     """T = 0 tokens: the layer returns an empty [0, H] output and launches nothing
