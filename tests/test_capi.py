@@ -9,7 +9,8 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "hkmoe.h")
-LIB = os.path.join(ROOT, "distributed-hipkittens_amd", "libhkmoe.so")
+# HKMOE_LIB: another build of the same library (the host-sanitizer run loads one)
+LIB = os.environ.get("HKMOE_LIB") or os.path.join(ROOT, "distributed-hipkittens_amd", "libhkmoe.so")
 
 
 def declared_functions():
