@@ -869,7 +869,7 @@ def summarize_counters(args):
                     "L1 waits on data from L2.\n\n")
             f.write("| kernel | CUs | L2 read requests | L2 read latency (cycles) | GPU cycles | requests in flight "
                     "per CU | TCP pending stall % |\n|---|---|---|---|---|---|---|\n")
-            ncu = {"grouped_gemm1": 192, "narrow_gemm1": 64, "narrow_gemm2": 64}
+            ncu = {} if dense else layer_cus(cfg)
             for lab in sorted(avg, key=lambda x: -avg[x].get("TCP_TCC_READ_REQ_sum", 0)):
                 a = avg[lab]
                 req, lat = a.get("TCP_TCC_READ_REQ_sum", 0.0), a.get("TCP_TCC_READ_REQ_LATENCY_sum", 0.0)
@@ -881,6 +881,28 @@ def summarize_counters(args):
                         f"{req / cyc / cus * lat / req:.0f} | "
                         f"{100 * a.get('TCP_PENDING_STALL_CYCLES_sum', 0.0) / (cyc * cus):.0f} |\n")
     print(json.dumps({"written": [os.path.relpath(out, ROOT)]}))
+
+
+def layer_cus(cfg, device_cus=256, narrow_cus=64, max_rows=64):
+    """CUs each kernel of a layer runs on, under the default narrow setting:
+    with narrow experts (at most max_rows rows) beside larger ones and T*k >
+    2*E*max_rows (two-stream schedule) the first 256x256 GEMM keeps
+    device_cus - narrow_cus and the narrow GEMMs take narrow_cus; otherwise
+    (no narrow expert, the one-stream schedule, or the MX layer, which has no
+    narrow path) every kernel has every CU.  The routing is the benched one
+    (host_draw), its top-k taken on the host (ties cannot occur on the drawn
+    floats)."""
+    import numpy as np
+    if cfg.get("mx") or not cfg["block"]:
+        return {}
+    _, logits = host_draw(cfg, 0)
+    k, E = cfg["k"], cfg["E"]
+    top = np.argpartition(-logits, k - 1, axis=1)[:, :k]
+    counts = np.bincount(top.ravel(), minlength=E)
+    narrow = int(((counts > 0) & (counts <= max_rows)).sum())
+    if narrow == 0 or cfg["T"] * k <= 2 * E * max_rows:
+        return {}
+    return {"grouped_gemm1": device_cus - narrow_cus, "narrow_gemm1": narrow_cus, "narrow_gemm2": narrow_cus}
 
 
 def dense_cpu_baseline(a_q, sa, b_q, sb, cfg, budget_s):
