@@ -1236,14 +1236,28 @@ int hkmoe_mx_gather_scales(const void* s, int64_t x_rows, int32_t k, const int32
                            int64_t rows, void* words, hkmoe_stream_t stream) {
   HK_REQUIRE(offsets && mtile_offsets, "mx_gather_scales: null pointer");
   HK_REQUIRE(rows == 0 || (s && words), "mx_gather_scales: null pointer");
-  HK_REQUIRE(k > 0 && k % kBK == 0, "mx_gather_scales: K=%d must be a multiple of 128", k);
+  HK_REQUIRE(k > 0 && k % kBK == 0 && k / 32 <= kMxGatherMaxKb,
+             "mx_gather_scales: K=%d must be a multiple of 128 and <= %d", k, 32 * kMxGatherMaxKb);
   HK_REQUIRE(num_experts >= 1 && num_experts <= kMaxExperts, "mx_gather_scales: bad E=%d", num_experts);
   HK_REQUIRE(rows >= 0 && rows < (1ll << 31) && x_rows >= 0, "mx_gather_scales: bad rows");
   HK_REQUIRE(gather != nullptr ? gather_div >= 1 : x_rows >= rows, "mx_gather_scales: bad gather");
+  HK_REQUIRE((reinterpret_cast<uintptr_t>(s) & 3) == 0, "mx_gather_scales: exponents must be 4-byte aligned");
   if (rows == 0) return HKMOE_OK;
   const int64_t ws = mx_words_per_step(rows, num_experts);
-  const int grid = static_cast<int>(std::min<int64_t>((ws * (k / kBK) + 255) / 256, 8192));
-  hk_launch(mx_gather_words_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+  // one workgroup per M tile (ws / 256 bounds their number), the tile's exponent
+  // rows in LDS
+  static bool attr_set[kMaxDevices] = {false};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  if (dev >= 0 && dev < kMaxDevices && !attr_set[dev]) {
+    const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(mx_gather_words_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 256 * kMxGatherMaxKb);
+    if (err != hipSuccess) return fail(HKMOE_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(err));
+    attr_set[dev] = true;
+  }
+  const int grid = static_cast<int>(std::min<int64_t>(ws / 256, 4096));
+  hk_launch(mx_gather_words_kernel, dim3(grid), dim3(256), static_cast<uint32_t>(256 * (k / 32)),
+            static_cast<hipStream_t>(stream),
                      static_cast<const uint8_t*>(s), k, gather, gather ? gather_div : 1, offsets, mtile_offsets,
                      num_experts, ws, static_cast<uint32_t*>(words));
   return check_launch("mx_gather_words_kernel");

@@ -725,37 +725,79 @@ __global__ __launch_bounds__(256) void mx_pack_weight_words_kernel(const uint8_t
 // r = 64*(q/64) + 16g + q%16 -- output row row0 + r, read from x row
 // gather[row0 + r] / gather_div (or row0 + r) -- for K block 4kt + (q%64)/16;
 // 0 for r >= valid.
+// One workgroup per M tile: the tile's expert is found once, its (gathered)
+// rows' exponent bytes are copied into LDS as whole rows (4-byte loads along
+// each row), and thread q then writes word q of every K step (consecutive
+// threads, consecutive words).  K <= 16384: at most 512 bytes per row.
+constexpr int kMxGatherMaxKb = 16384 / 32;
 __global__ __launch_bounds__(256) void mx_gather_words_kernel(const uint8_t* __restrict__ s, int K,
                                                               const int32_t* __restrict__ gather, int gather_div,
                                                               const int32_t* __restrict__ offsets,
                                                               const int32_t* __restrict__ mtile_offsets,
                                                               int num_experts, int64_t ws_rs,
                                                               uint32_t* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t rows_s[];  // [256][kb] exponent bytes
+  __shared__ int s_row0, s_valid;
+  __shared__ int64_t xrow_s[256];  // x row of each tile row, -1 past `valid`
   const int kb = K / 32, ks = K / 128;
-  const int64_t n_words = static_cast<int64_t>(mtile_offsets[num_experts]) * 256;
-  const int64_t total = n_words * ks;
-  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
-    const int kt = static_cast<int>(i / n_words);
-    const int64_t w = i - static_cast<int64_t>(kt) * n_words;
-    const int m = static_cast<int>(w >> 8), q = static_cast<int>(w & 255);
-    int lo = 0, hi = num_experts;  // largest e with mtile_offsets[e] <= m
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (mtile_offsets[mid] <= m) lo = mid; else hi = mid;
-    }
-    const int row0 = offsets[lo] + (m - mtile_offsets[lo]) * 256;
-    const int valid = min(256, offsets[lo + 1] - row0);
-    const int blk = 4 * kt + ((q >> 4) & 3);
-    uint32_t v = 0;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int r = (q & ~63) + 16 * g + (q & 15);
-      if (r < valid) {
-        const int64_t xr = gather ? gather[row0 + r] / gather_div : row0 + r;
-        v |= static_cast<uint32_t>(s[xr * kb + blk]) << (8 * g);
+  const int n_mt = mtile_offsets[num_experts];
+  const int tid = threadIdx.x;
+  for (int m = blockIdx.x; m < n_mt; m += gridDim.x) {
+    if (tid == 0) {
+      int lo = 0, hi = num_experts;  // largest e with mtile_offsets[e] <= m
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (mtile_offsets[mid] <= m) lo = mid; else hi = mid;
       }
+      const int row0 = offsets[lo] + (m - mtile_offsets[lo]) * 256;
+      s_row0 = row0;
+      s_valid = min(256, offsets[lo + 1] - row0);
     }
-    out[static_cast<int64_t>(kt) * ws_rs + w] = v;
+    __syncthreads();
+    {
+      const int row0 = s_row0, valid = s_valid;
+      xrow_s[tid] = tid < valid ? (gather ? gather[row0 + tid] / gather_div : row0 + tid) : -1;
+    }
+    __syncthreads();
+    // the rows' bytes in chunks of 16 (K a multiple of 512 and s 16-byte
+    // aligned) or 4, up to 16 loads in flight per thread; rows past `valid`
+    // read as zero bytes
+    auto copy_rows = [&](auto chunk_tag) __attribute__((always_inline)) {
+      using C = decltype(chunk_tag);
+      constexpr int kC = sizeof(C);
+      const int per_row = kb / kC, total = 256 * per_row;
+      for (int base = 0; base < total; base += 256 * 16) {
+        C v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int i = base + u * 256 + tid;
+          v[u] = C{};
+          if (i < total) {
+            const int r = i / per_row, c = i - r * per_row;
+            const int64_t xr = xrow_s[r];
+            if (xr >= 0) v[u] = reinterpret_cast<const C*>(s + xr * kb)[c];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int i = base + u * 256 + tid;
+          if (i < total) reinterpret_cast<C*>(rows_s)[i] = v[u];
+        }
+      }
+    };
+    if (kb % 16 == 0 && (reinterpret_cast<uintptr_t>(s) & 15) == 0) copy_rows(uint4{}); else copy_rows(uint32_t{});
+    __syncthreads();
+    const int q = tid;
+    const int rbase = (q & ~63) + (q & 15), bsub = (q >> 4) & 3;
+    uint32_t* dst = out + static_cast<int64_t>(m) * 256 + q;
+    for (int kt = 0; kt < ks; ++kt) {
+      const int blk = 4 * kt + bsub;
+      uint32_t v = 0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) v |= static_cast<uint32_t>(rows_s[(rbase + 16 * g) * kb + blk]) << (8 * g);
+      dst[static_cast<int64_t>(kt) * ws_rs] = v;
+    }
+    __syncthreads();  // rows_s is rewritten for the next M tile
   }
 }
 
