@@ -8,10 +8,13 @@ GPU's hq) and the combine (from the GPU's y) within 1e-2 of the fp32 values;
 the one-call layer, the stepwise layer and packed vs row-major weights give
 identical bits.
 
-End to end against an independent oracle run the bound is E2E_TOL = 3e-2: the
-MX requantisation of h rounds to 3-bit mantissas under power-of-two block
-scales, so a one-ulp bf16 difference in h (fp32 accumulation order) can move an
-element of hq by a whole e4m3 step (up to 6.25%), and those steps reach y.
+End to end against an independent oracle run, at config 3's shapes (I = 2048)
+the sampled tokens meet TOL (2.8e-3 measured).  The small shapes below (I of
+128-384) are held to E2E_TOL = 3e-2: the MX requantisation of h rounds to
+3-bit mantissas under power-of-two block scales, so a one-ulp bf16 difference
+in h (fp32 accumulation order) can move an element of hq by a whole e4m3 step
+(up to 6.25%), and with few terms per output one such step weighs more (1.0e-3
+to 1.03e-2 measured over three seeds of each case).
 """
 import numpy as np
 import pytest
@@ -173,4 +176,4 @@ def test_mx_layer_dsv3_shape_sampled(hk):
             acc += wts[t, j] * fp8.bf16_round(y.astype(np.float32))[0]
         ref[n] = acc
     got = bf16_np(out[torch.from_numpy(toks).cuda()])
-    assert rel_err(got, ref) <= E2E_TOL
+    assert rel_err(got, ref) <= TOL
