@@ -415,28 +415,44 @@ __global__ __launch_bounds__(256) void requant_group_kernel(const uint16_t* __re
   }
 }
 
-// per-tensor: amax was accumulated by GEMM 1; 8 elements per thread.
+// per-tensor: amax was accumulated by GEMM 1 over the bf16-rounded h, so s is
+// the scale of a bf16 maximum and every x is a bf16 value: the division-free
+// quotient (QuotScale) gives the bytes of x / s there, as the GEMM epilogues'
+// self-check establishes for that domain.  8 elements per 16-byte chunk; each
+// thread issues its 4 chunks' loads (read once: non-temporal) before
+// converting any, so 4 KiB per wave are in flight.
 __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __restrict__ h,
                                                              int64_t n8, const float* amax,
                                                              uint8_t* __restrict__ hq,
                                                              float* __restrict__ hs) {
+  constexpr int kU = 4;
   const float s = scale_from_amax(*amax);
+  const QuotScale qs = quot_scale(s);
   if (blockIdx.x == 0 && threadIdx.x == 0) hs[0] = s;
-  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n8; i += static_cast<int64_t>(gridDim.x) * 256) {
-    const uint4 v = reinterpret_cast<const uint4*>(h)[i];
+  auto convert = [&](uint4 v) __attribute__((always_inline)) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint2 o;
     uint32_t* op = &o.x;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const uint32_t p0 = w[q * 2], p1 = w[q * 2 + 1];
-      op[q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(p0 & 0xffffu), s),
-                          quot_e4m3(bf16_bits_to_f32(p0 >> 16), s),
-                          quot_e4m3(bf16_bits_to_f32(p1 & 0xffffu), s),
-                          quot_e4m3(bf16_bits_to_f32(p1 >> 16), s));
+      op[q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(p0 & 0xffffu), qs),
+                          quot_e4m3(bf16_bits_to_f32(p0 >> 16), qs),
+                          quot_e4m3(bf16_bits_to_f32(p1 & 0xffffu), qs),
+                          quot_e4m3(bf16_bits_to_f32(p1 >> 16), qs));
     }
-    reinterpret_cast<uint2*>(hq)[i] = o;
+    return o;
+  };
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  int64_t i = blockIdx.x * 256ll + threadIdx.x;
+  for (; i + (kU - 1) * stride < n8; i += kU * stride) {
+    uint4 v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) v[u] = ld_nt16(h + (i + u * stride) * 8);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) reinterpret_cast<uint2*>(hq)[i + u * stride] = convert(v[u]);
   }
+  for (; i < n8; i += stride) reinterpret_cast<uint2*>(hq)[i] = convert(ld_nt16(h + i * 8));
 }
 
 // ---------------------------------------------------------------------------
