@@ -418,9 +418,11 @@ __global__ __launch_bounds__(256) void requant_group_kernel(const uint16_t* __re
 // per-tensor: amax was accumulated by GEMM 1 over the bf16-rounded h, so s is
 // the scale of a bf16 maximum and every x is a bf16 value: the division-free
 // quotient (QuotScale) gives the bytes of x / s there, as the GEMM epilogues'
-// self-check establishes for that domain.  8 elements per 16-byte chunk; each
-// thread issues its 4 chunks' loads (read once: non-temporal) before
-// converting any, so 4 KiB per wave are in flight.
+// self-check establishes for that domain.  One case lies outside it: an
+// infinite x with a finite s (amax NaN, s = 1), where x / s is x (saturated by
+// the conversion) and the remainder step would give NaN.  8 elements per
+// 16-byte chunk; each thread issues its 4 chunks' loads (read once:
+// non-temporal) before converting any, so 4 KiB per wave are in flight.
 __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __restrict__ h,
                                                              int64_t n8, const float* amax,
                                                              uint8_t* __restrict__ hq,
@@ -428,7 +430,13 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
   constexpr int kU = 4;
   const float s = scale_from_amax(*amax);
   const QuotScale qs = quot_scale(s);
+  const bool s_finite = !__builtin_isinf(s);
   if (blockIdx.x == 0 && threadIdx.x == 0) hs[0] = s;
+  auto quot = [&](uint32_t bits) __attribute__((always_inline)) {
+    const float x = bf16_bits_to_f32(bits);
+    const float q = quot_e4m3(x, qs);
+    return (s_finite && __builtin_isinf(x)) ? x : q;
+  };
   auto convert = [&](uint4 v) __attribute__((always_inline)) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint2 o;
@@ -436,10 +444,7 @@ __global__ __launch_bounds__(256) void requant_tensor_kernel(const uint16_t* __r
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const uint32_t p0 = w[q * 2], p1 = w[q * 2 + 1];
-      op[q] = pack_e4m3x4(quot_e4m3(bf16_bits_to_f32(p0 & 0xffffu), qs),
-                          quot_e4m3(bf16_bits_to_f32(p0 >> 16), qs),
-                          quot_e4m3(bf16_bits_to_f32(p1 & 0xffffu), qs),
-                          quot_e4m3(bf16_bits_to_f32(p1 >> 16), qs));
+      op[q] = pack_e4m3x4(quot(p0 & 0xffffu), quot(p0 >> 16), quot(p1 & 0xffffu), quot(p1 >> 16));
     }
     return o;
   };

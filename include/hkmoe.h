@@ -167,7 +167,8 @@ int hkmoe_grouped_gemm1(const void* x, const float* x_scale, const int32_t* gath
  * Requantise a bf16 intermediate to e4m3 for GEMM 2.
  *   TENSOR: hs[0] = scale(amax), hq = e4m3(h / hs[0]) (amax from GEMM 1).
  *   BLOCK:  1x128 groups, hs_t [I/128, R] (transposed) = scale(amax_g).
- *   scale(a) = max(a / 448, 2^-126), or 1 for a == 0.
+ *   scale(a) = max(a / 448, 2^-126), or 1 for a == 0 (and for a NaN a).
+ *   A NaN h gives +-448 (0x7E | sign) rather than the NaN code.
  */
 int hkmoe_requant(const void* h, int64_t rows, int32_t inter, int scale_mode, const float* amax,
                   void* hq, float* hs, hkmoe_stream_t stream);
@@ -378,6 +379,8 @@ int hkmoe_moe_forward_noalloc(const void* x_q, const float* x_scale, const float
  *   hkmoe_quant_block:  q [B,R,C] e4m3, s [B, R/128, C/128] (128x128 blocks)
  *   hkmoe_quant_tensor: q [R,C], s [1]; amax_ws: one fp32 of device scratch.
  * Scale = amax/448 (1.0 for an all-zero block); q = e4m3(x / s) RNE, saturating.
+ * Bit-exact for finite x; a NaN gives +-448 (0x7E | sign), and block maxima
+ * skip NaNs.
  */
 int hkmoe_quant_group(const float* x, int64_t rows, int64_t cols, void* q, float* s,
                       hkmoe_stream_t stream);

@@ -382,6 +382,40 @@ def test_requant_large_bit_exact(hk, block):
         assert _np(hs)[0] == s_ref
 
 
+@pytest.mark.parametrize("case", ["finite", "inf", "nan"])
+def test_requant_tensor_special_values(hk, case):
+    """Per-tensor requantisation with infinities and NaNs in h, against the
+    specification's bytes: an infinite h makes amax and s infinite (finite x
+    give signed zeros); a NaN makes amax NaN and s = 1, so an infinite x
+    saturates to +-448.  Signed zeros and values next to the saturation point
+    ride along.  Where the specification's quotient is NaN (a NaN x, or
+    inf / inf) the device conversion's clamp gives +-448 (0x7E | sign), not the
+    NaN code 0x7F, as documented for non-finite inputs."""
+    rng = np.random.default_rng(5)
+    rows, inter = 64, 2048
+    h = (rng.standard_normal((rows, inter)) * 40).astype(np.float32)
+    h[0, :8] = [0.0, -0.0, 448.0, -448.0, 464.0, -464.0, 465.0, 1e-30]
+    if case in ("inf", "nan"):
+        h[1, :4] = [np.inf, -np.inf, np.inf, -np.inf]
+    if case == "nan":
+        h[2, :2] = [np.nan, -np.nan]
+    h = spec.bf16_round(h)
+    hb = torch.from_numpy(h).to(torch.bfloat16).cuda()
+    hq = torch.empty((rows, inter), dtype=torch.float8_e4m3fn, device="cuda")
+    hs = torch.empty(1, dtype=torch.float32, device="cuda")
+    amax = torch.tensor([float(np.max(np.abs(h)))], dtype=torch.float32, device="cuda")
+    hk.tk_kernel.dispatch_requant(hb, amax, hq, hs)
+    torch.cuda.synchronize()
+    with np.errstate(invalid="ignore"):
+        q_ref, s_ref = spec.requant(h, False)
+    got = f8_np(hq)
+    nan = (q_ref & 0x7F) == 0x7F
+    assert nan.sum() == {"finite": 0, "inf": 4, "nan": 2}[case]
+    np.testing.assert_array_equal(got[~nan], q_ref[~nan])
+    np.testing.assert_array_equal(got[nan] & 0x7F, np.full(int(nan.sum()), 0x7E, np.uint8))
+    assert _np(hs)[0] == s_ref
+
+
 def test_routing_ties_and_edges(hk):
     """Ties resolve to the lower expert id; T not a multiple of the block; E not a power of 2."""
     rng = np.random.default_rng(3)
