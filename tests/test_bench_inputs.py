@@ -4,6 +4,11 @@ bench.host_draw restates oracle/synth.py's first draws (x, logits, Zipf bias
 permutation) because the benchmark may not import the oracle; these tests pin
 the two together, so the benched routing is the specification's draw.
 """
+import json
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 
@@ -35,3 +40,15 @@ def test_dsv3_draw_routing_profile():
     assert (counts == 0).sum() == 69
     assert counts.max() == 7970
     assert ((counts > 0) & (counts <= 64)).sum() == 136
+
+
+@pytest.mark.parametrize("n", [2, 8])
+def test_bench_refuses_more_than_one_gpu(n):
+    """--gpus N > 1 exits with status 2 and a one-line JSON message, before
+    touching torch or the GPU (the build measures one GPU only)."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", str(n)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
