@@ -241,7 +241,7 @@ __device__ __forceinline__ void fold_block(f32x4& c, const f32x4& p, float f) {
 // next tile's claim and lookups) is used later; otherwise one asm statement,
 // which it cannot see into.  Tracked, the gate/up GEMM with block scales is
 // 1.0-1.4% faster and the per-tensor one 0.5%; the bf16-store and MX GEMMs
-// measured slower tracked (+1.5%, +0.8%) and keep the asm form.
+// measured slower tracked (+0.8-1.5%, +0.8%) and keep the asm form.
 constexpr int kWaitVm0Lgkm0 = 0x0070;  // s_waitcnt vmcnt(0) lgkmcnt(0)
 constexpr int kWaitVm4Lgkm0 = 0x0074;  // s_waitcnt vmcnt(4) lgkmcnt(0)
 constexpr int kWaitLgkm0 = 0xC07F;     // s_waitcnt lgkmcnt(0)
